@@ -1,0 +1,111 @@
+/*
+ * qwen38_kv.h -- C ABI of the MI355X (gfx950) quantized KV-cache path: the append/evict half (q8 window ring plus the
+ * 4..8-bit packed long-term store, optional 256-point Walsh-Hadamard rotation) and the gather+attention half (split-K
+ * GQA decode attention over the mixed store, 1..8 query tokens, paged multi-sequence).
+ *
+ * Conventions (the reference's C API, capi.cpp:190-263): an opaque handle; int status, >= 0 success, -1 error with the
+ * message in the thread-local mk_last_error(); no exception crosses the ABI; caller-owned output buffers with a cap,
+ * and cap 0 / NULL returns the count needed.  Device pointers are HIP device addresses already resident in HBM;
+ * `stream` is a hipStream_t (NULL: the default stream).  One handle is not thread-safe: calls on it are serialised by
+ * the caller, as with the reference's engine.
+ *
+ * Shapes: NKV = 4 kv heads, NH = 24 query heads (GQA 6), head dim 256, up to 17 attention slots (layers), up to 8
+ * query tokens per attend call, up to 8 sequences per attend call.
+ */
+#ifndef QWEN38_KV_H
+#define QWEN38_KV_H
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Last error of this thread.  Replaces mk_last_error, capi.cpp:263. */
+const char * mk_last_error(void);
+
+/*
+ * Create a KV store.  Replaces the KV block of mk_new_mtp / MKEngine construction (capi.cpp:266, loader.cu:1329-1510).
+ *   kv_spec   the MK_KV grammar: comma-separated <K|V|*><slot>=<4..8>[r] (slot 0..n_layers-1, * or empty: all;
+ *             r: stored Walsh-Hadamard rotated); NULL or "" = every side q8 (loader.cu:1329-1365)
+ *   win       MK_KV_WIN: low-bit sides keep their newest >= win positions as q8 in a ring of
+ *             (ceil(win/640)+1)*640+32 rows per kv head (loader.cu:1469-1510); 0 = no window
+ *   win_all   MK_KV_WIN_ALL: rings for the q8 sides too (test knob, loader.cu:1487-1490)
+ *   n_layers  attention slots, 1..17
+ *   n_seq     sequences (lanes), 1..64
+ *   ctx       positions per sequence
+ *   page      positions per page, a multiple of 32; 0 = one contiguous page per sequence (the reference's
+ *             [kv head][ctx][row] layout)
+ *   n_pages   pages in the shared pool; 0 = n_seq * ceil(ctx / page).  Each sequence starts with the identity table
+ *             over its own range of pages (when the pool is large enough).
+ * Returns NULL on error (mk_last_error).
+ */
+void * mk_kv_new(const char * kv_spec, int win, int win_all, int n_layers, int n_seq, int ctx, int page, int n_pages);
+
+/* Free a store (replaces mk_free, capi.cpp:418).  NULL is a no-op. */
+void mk_free(void * h);
+
+/* Set the page table of one sequence: logical page i -> physical page pages[i] (host array, n <= ceil(ctx/page)).
+ * No counterpart in the reference (its lanes are contiguous, lanes.cu:290-345); added for paged multi-sequence. */
+int mk_kv_set_pages(void * h, int seq, const int * pages, int n);
+
+/*
+ * Append T positions pos .. pos+T-1 of sequence seq for slots layer0 .. layer0+n_layers-1.  k, v: device arrays
+ * [T][n_layers][4][256] of fp32 (dtype 0) or fp16 (dtype 1), the rows after RMSNorm/RoPE.  Each row is stored in its
+ * side's format (optionally rotated) and, for sides with a window, as q8 in the ring.  Replaces the kv_store step of
+ * mk_step / mk_prefill (capi.cpp:508-554 -> qwen38_mk.cu:2099-2116, 2955-2985).  Asynchronous on `stream`.
+ */
+int mk_kv_append(void * h, int seq, int layer0, int n_layers, int pos, int T, const void * k, const void * v, int dtype, void * stream);
+
+/*
+ * Decode attention for n_seq sequences (seqs[i], context lens[i] after this call's T rows) over slots layer0 ..
+ * layer0+n_layers-1.  q: device [n_layers][n_seq][T][24][256] fp32 (after RMSNorm/RoPE, before the 1/16 scale);
+ * out: device, same shape, the attention output before the output gate (V un-rotated when V is stored rotated).
+ * Token t of a sequence sees positions <= lens[i] - T + t.  The T rows must share one 640-position window bucket
+ * (att_cap_T, mk_shared.cuh:288-291; see mk_kv_cap_T).  Replaces attn_core + attn_combine of mk_step
+ * (qwen38_mk.cu:4568-4700).  Asynchronous on `stream`.
+ */
+int mk_kv_attend(void * h, int layer0, int n_layers, int n_seq, const int * seqs, const int * lens, int T, const float * q, float * out,
+                 void * stream);
+
+/* Rewind sequence 0 / sequence seq to position pos: ring rows refilled from the main store (ring_rewind,
+ * ck_pool.cu:285-296; k_ring_refill, qwen38_mk.cu:2485-2517).  mk_truncate / mk_rewind_to replace capi.cpp:572 / 601. */
+int mk_truncate(void * h, int len);
+int mk_rewind_to(void * h, int pos);
+int mk_kv_rewind(void * h, int seq, int pos);
+
+/* Bytes per KV token (all slots, both sides, values + scales), of the window rings, of the recurrent state (0: none in
+ * this store) and of one checkpoint (0).  Replaces mk_kv_sizes, capi.cpp:675. */
+void mk_kv_sizes(void * h, long long * per_token, long long * rings, long long * state, long long * checkpoint);
+
+/* 64-bit digests of the KV state of sequence 0 / seq (the reference's layout restricted to the KV rows, engine.cu:1436-1514):
+ * words [0x4d4b444701, n, 0, kvrc, ring_lo, n_layers, 4, 0], then per (slot, side, kv head, p < n) the main row's hash,
+ * then per (slot, side, kv head, ring_lo <= p < n) the ring row's hash (0 for sides without a ring).  Returns the word
+ * count (writes up to cap).  Replaces mk_state_digest, capi.cpp:635. */
+int mk_state_digest(void * h, unsigned long long * out, int cap);
+int mk_kv_state_digest(void * h, int seq, unsigned long long * out, int cap);
+
+/* Copy n logical rows (positions p0 .. p0+n-1) of one (slot, side w, kv head g) to host memory: from the main store
+ * (ring = 0; vals n * 32 * bits bytes) or the window ring (ring = 1; n * 256 bytes); scales n * 8 fp16.  Returns the
+ * row bytes.  Test and park/unpark helper (host_store.cu:80-160 copies the same rows). */
+int mk_kv_read_rows(void * h, int seq, int layer, int w, int g, int p0, int n, int ring, void * vals, unsigned short * scales);
+
+/* Knobs: "max_blocks" caps the attention grid (0: one workgroup per work item); results never depend on it. */
+int mk_kv_config(void * h, const char * key, long long value);
+
+/* Kernel timing with HIP events on the launch stream (the reference's MK_PROFILE per-phase means, engine.cu:382-506).
+ * enable = 1 resets and starts recording every attend call's query-prep, attention and combine kernels; 0 stops.
+ * out[0..5): calls, then total milliseconds of query prep, attention, combine, append.  Returns the count written. */
+int mk_kv_profile(void * h, int enable, double * out, int cap);
+
+/* Host-only geometry and grammar helpers (no GPU needed). */
+int mk_kv_window_start(int L, int win);  /* kv_ws, qwen38_mk.cu:2118-2126 */
+int mk_kv_ring_rows(int win);            /* kvrc, loader.cu:1479-1486 */
+int mk_kv_cap_T(int n, int T);           /* att_cap_T, mk_shared.cuh:288-291 */
+/* Parse an MK_KV spec for n_layers slots: out[0..n) K bits, [n..2n) V bits, [2n..3n) K rotated, [3n..4n) V rotated.
+ * Returns 0, or -1 with mk_last_error (loader.cu:1329-1365's messages). */
+int mk_kv_parse_spec(const char * kv_spec, int n_layers, int * out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,562 @@
+// C ABI of the KV path: store construction (MK_KV grammar, pools, window rings, page tables), append, attend, rewind,
+// sizes, digest.  Conventions follow the reference's capi.cpp: -1 plus a thread-local message, no exception crosses the
+// boundary (guarded, capi.cpp:222-245).  The store is the product's own C++ host runtime; the arithmetic is in the HIP
+// kernels (kv_store.hip, kv_attn.hip).
+#include "../../include/qwen38_kv.h"
+#include "kv_launch.h"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdint>
+#include <cstdlib>
+#include <cstring>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+using namespace qkv;
+
+namespace {
+
+thread_local std::string g_err;
+
+struct HipError : std::runtime_error {
+    using std::runtime_error::runtime_error;
+};
+
+#define HCK(x)                                                                                                         \
+    do {                                                                                                               \
+        const hipError_t e_ = (x);                                                                                     \
+        if (e_ != hipSuccess) throw HipError(std::string(#x) + ": " + hipGetErrorString(e_));                         \
+    } while (0)
+
+constexpr int SLOTS = 17;
+constexpr int ATT_BUCKET_ = 640;
+constexpr int ATP_ = 32;
+
+struct Spec {
+    int kb[SLOTS], vb[SLOTS], kr[SLOTS], vr[SLOTS];
+};
+
+// MK_KV grammar (loader.cu:1329-1365): <K|V|*><slot>=<4..8>[r], comma separated; slot empty or * = all slots
+void parse_spec(const char * spec, int n_layers, Spec & s) {
+    for (int i = 0; i < SLOTS; i++) {
+        s.kb[i] = s.vb[i] = 8;
+        s.kr[i] = s.vr[i] = 0;
+    }
+    if (!spec || !spec[0]) return;
+    const std::string str = spec;
+    size_t i = 0;
+    while (i < str.size()) {
+        size_t j = str.find(',', i);
+        if (j == std::string::npos) j = str.size();
+        const std::string tok = str.substr(i, j - i);
+        i = j + 1;
+        if (tok.empty()) continue;
+        const size_t e = tok.find('=');
+        if (e == std::string::npos || e == 0 || !strchr("KV*", tok[0])) throw std::runtime_error("MK_KV: bad item " + tok);
+        const std::string sl = tok.substr(1, e - 1), md = tok.substr(e + 1);
+        if (md.empty() || md.size() > 2 || md[0] < '4' || md[0] > '8' || (md.size() == 2 && md[1] != 'r'))
+            throw std::runtime_error("MK_KV: expected 4..8 or 4r..8r in " + tok);
+        const bool rot = md.size() == 2;
+        const bool all = sl.empty() || sl == "*";
+        long slot = -1;
+        if (!all) {
+            char * end = nullptr;
+            slot = strtol(sl.c_str(), &end, 10);
+            if (*end || slot < 0 || slot >= n_layers)
+                throw std::runtime_error("MK_KV: bad slot in " + tok + " (0.." + std::to_string(n_layers - 1) + " or *)");
+        }
+        for (int w = 0; w < 2; w++)
+            if (tok[0] == '*' || tok[0] == "KV"[w])
+                for (int k = 0; k < n_layers; k++)
+                    if (all || k == slot) {
+                        (w ? s.vb : s.kb)[k] = md[0] - '0';
+                        (w ? s.vr : s.kr)[k] = rot;
+                    }
+    }
+}
+
+int window_start(int L, int win) {
+    if (win <= 0) return 0;
+    const int ws = (L + ATT_BUCKET_ - 1) / ATT_BUCKET_ - 1 - (win + ATT_BUCKET_ - 1) / ATT_BUCKET_;
+    return ws > 0 ? ws * ATT_BUCKET_ : 0;
+}
+int ring_rows(int win) { return win > 0 ? ((win + ATT_BUCKET_ - 1) / ATT_BUCKET_ + 1) * ATT_BUCKET_ + ATP_ : 0; }
+
+uint64_t dg_hash(const void * p, size_t nb, uint64_t h = 0xcbf29ce484222325ULL) { // engine.cu:1444-1456
+    const unsigned char * b = static_cast<const unsigned char *>(p);
+    size_t i = 0;
+    for (; i + 8 <= nb; i += 8) {
+        uint64_t w;
+        memcpy(&w, b + i, 8);
+        h = (h ^ w) * 0x100000001b3ULL;
+        h ^= h >> 31;
+    }
+    for (; i < nb; i++) h = (h ^ b[i]) * 0x100000001b3ULL;
+    return h;
+}
+
+struct Store {
+    int n_layers = 0, n_seq = 0, ctx = 0, page = 0, n_pages = 0, pt_stride = 0, win = 0, kvrc = 0, win_all = 0;
+    Spec spec{};
+    StoreLayout S{};
+    std::vector<int> ptab;
+    int * ptab_dev = nullptr;
+    std::vector<int> n, top; // per sequence: committed length, rows written (ring_rewind's kv_top)
+    std::vector<void *> allocs;
+    size_t ring_bytes = 0;
+    // workspace of attend (grown on demand)
+    void * qh = nullptr;
+    size_t qh_bytes = 0;
+    void * part = nullptr;
+    size_t part_bytes = 0;
+    void * ml = nullptr;
+    size_t ml_bytes = 0;
+    int max_blocks = 0;
+    // mk_kv_profile: a pool of event sets recorded around each call's kernels on the launch stream; a set's elapsed times
+    // are read only when the pool wraps around or profiling stops, so timed back-to-back calls never wait on the host
+    struct EvSet {
+        hipEvent_t e[4] = {};
+        int kind = 0; // 0 free, 1 attend (qprep | attention | combine), 2 append
+    };
+    static constexpr int NEV = 256;
+    int prof = 0;
+    double prof_acc[5] = {0, 0, 0, 0, 0}; // calls, qprep, attention, combine, append (ms)
+    std::vector<EvSet> evs;
+    int ev_next = 0;
+
+    void * dalloc(size_t bytes) {
+        void * p = nullptr;
+        HCK(hipMalloc(&p, std::max<size_t>(bytes, 256)));
+        allocs.push_back(p);
+        HCK(hipMemset(p, 0, std::max<size_t>(bytes, 256)));
+        return p;
+    }
+    ~Store() {
+        for (EvSet & es : evs)
+            for (hipEvent_t e : es.e)
+                if (e) (void) hipEventDestroy(e);
+        for (void * p : allocs) (void) hipFree(p);
+        if (qh) (void) hipFree(qh);
+        if (part) (void) hipFree(part);
+        if (ml) (void) hipFree(ml);
+    }
+    void grow(void *& p, size_t & have, size_t need) {
+        if (need <= have) return;
+        HCK(hipDeviceSynchronize()); // the old buffer may still be read by enqueued work
+        if (p) HCK(hipFree(p));
+        p = nullptr;
+        have = 0;
+        HCK(hipMalloc(&p, need));
+        have = need;
+    }
+    size_t main_row(int seq, int g, int p) const {
+        const int lp = p / page;
+        return (size_t) (g * n_pages + ptab[(size_t) seq * pt_stride + lp]) * page + (p - lp * page);
+    }
+};
+
+void prof_read(Store & s, Store::EvSet & es) {
+    if (!es.kind) return;
+    float ms = 0.f;
+    if (es.kind == 1) {
+        HCK(hipEventSynchronize(es.e[3]));
+        s.prof_acc[0] += 1;
+        for (int i = 0; i < 3; i++) {
+            HCK(hipEventElapsedTime(&ms, es.e[i], es.e[i + 1]));
+            s.prof_acc[1 + i] += ms;
+        }
+    } else {
+        HCK(hipEventSynchronize(es.e[1]));
+        HCK(hipEventElapsedTime(&ms, es.e[0], es.e[1]));
+        s.prof_acc[4] += ms;
+    }
+    es.kind = 0;
+}
+
+// the event set of the next profiled call (nullptr when profiling is off)
+Store::EvSet * prof_set(Store & s, int kind) {
+    if (!s.prof) return nullptr;
+    Store::EvSet & es = s.evs[(size_t) s.ev_next];
+    s.ev_next = (s.ev_next + 1) % Store::NEV;
+    prof_read(s, es); // (only when the pool wrapped around)
+    es.kind = kind;
+    return &es;
+}
+
+void prof_mark(Store::EvSet * es, int i, hipStream_t st) {
+    if (es) HCK(hipEventRecord(es->e[i], st));
+}
+
+Store * as_store(void * h) {
+    if (!h) throw std::runtime_error("null KV store handle");
+    return static_cast<Store *>(h);
+}
+
+template <class F> int guarded(F f) {
+    try {
+        return f();
+    } catch (const std::exception & e) {
+        g_err = e.what();
+        return -1;
+    }
+}
+
+void check_seq(const Store & s, int seq) {
+    if (seq < 0 || seq >= s.n_seq) throw std::runtime_error("sequence " + std::to_string(seq) + " out of range 0.." + std::to_string(s.n_seq - 1));
+}
+void check_layers(const Store & s, int layer0, int nl) {
+    if (nl < 1 || layer0 < 0 || layer0 + nl > s.n_layers)
+        throw std::runtime_error("layers " + std::to_string(layer0) + " .. " + std::to_string(layer0 + nl - 1) + " outside 0.." +
+                                 std::to_string(s.n_layers - 1));
+}
+
+int rewind_seq(Store & s, int seq, int P) {
+    check_seq(s, seq);
+    if (P < 0) throw std::runtime_error("negative rewind position");
+    if (s.kvrc > 0) { // ring_rewind, ck_pool.cu:285-296
+        const int p0 = std::max(0, P - s.kvrc), p1 = std::min(P, s.top[seq] - s.kvrc);
+        if (p1 > p0) {
+            HCK(launch_ring_refill(s.S, seq, s.n_layers, p0, p1, nullptr));
+            HCK(hipDeviceSynchronize());
+        }
+    }
+    s.top[seq] = std::min(s.top[seq], P);
+    s.n[seq] = std::min(s.n[seq], P);
+    return 0;
+}
+
+int digest_seq(Store & s, int seq, unsigned long long * out, int cap) {
+    check_seq(s, seq);
+    HCK(hipDeviceSynchronize());
+    const int nn = s.n[seq], rc = s.kvrc, rlo = rc ? std::max(0, nn - rc) : nn;
+    std::vector<unsigned long long> v = {0x4d4b444701ULL, (unsigned long long) nn, 0ULL, (unsigned long long) rc, (unsigned long long) rlo,
+                                         (unsigned long long) s.n_layers, (unsigned long long) NKV, 0ULL};
+    std::vector<unsigned char> vb;
+    std::vector<uint16_t> sb;
+    for (int l = 0; l < s.n_layers; l++)
+        for (int w = 0; w < 2; w++) {
+            const SideLayout & sd = s.S.side[l][w];
+            const size_t rb = (size_t) row_bytes(sd.bits);
+            for (int g = 0; g < NKV; g++) {
+                vb.resize(std::max<size_t>(1, (size_t) nn * rb));
+                sb.resize(std::max<size_t>(1, (size_t) nn * 8));
+                for (int p = 0; p < nn;) { // page by page: rows of a page are contiguous
+                    const int cnt = std::min(nn - p, s.page - p % s.page);
+                    const size_t r = s.main_row(seq, g, p);
+                    HCK(hipMemcpy(vb.data() + (size_t) p * rb, sd.vals + r * rb, (size_t) cnt * rb, hipMemcpyDeviceToHost));
+                    HCK(hipMemcpy(sb.data() + (size_t) p * 8, sd.scs + r * 8, (size_t) cnt * 16, hipMemcpyDeviceToHost));
+                    p += cnt;
+                }
+                for (int p = 0; p < nn; p++) v.push_back(dg_hash(sb.data() + (size_t) p * 8, 16, dg_hash(vb.data() + (size_t) p * rb, rb)));
+            }
+        }
+    for (int l = 0; l < s.n_layers; l++)
+        for (int w = 0; w < 2; w++) {
+            const SideLayout & sd = s.S.side[l][w];
+            for (int g = 0; g < NKV; g++) {
+                if (!rc || !sd.ring) {
+                    v.insert(v.end(), (size_t) (nn - rlo), 0ULL);
+                    continue;
+                }
+                std::vector<int8_t> rv((size_t) rc * HD);
+                std::vector<uint16_t> rs((size_t) rc * 8);
+                const size_t base = (size_t) (seq * NKV + g) * rc;
+                HCK(hipMemcpy(rv.data(), sd.ring + base * HD, rv.size(), hipMemcpyDeviceToHost));
+                HCK(hipMemcpy(rs.data(), sd.rsc + base * 8, rs.size() * 2, hipMemcpyDeviceToHost));
+                for (int p = rlo; p < nn; p++) {
+                    const size_t r = (size_t) (p % rc);
+                    v.push_back(dg_hash(rs.data() + r * 8, 16, dg_hash(rv.data() + r * HD, HD)));
+                }
+            }
+        }
+    if (out)
+        for (int i = 0; i < std::min((int) v.size(), cap); i++) out[i] = v[(size_t) i];
+    return (int) v.size();
+}
+
+} // namespace
+
+extern "C" {
+
+const char * mk_last_error(void) { return g_err.c_str(); }
+
+int mk_kv_window_start(int L, int win) { return window_start(L, win); }
+int mk_kv_ring_rows(int win) { return ring_rows(win); }
+int mk_kv_cap_T(int n, int T) {
+    const int lim = ATT_BUCKET_ * ((n + ATT_BUCKET_) / ATT_BUCKET_) - n;
+    return T < lim ? T : lim;
+}
+
+int mk_kv_parse_spec(const char * kv_spec, int n_layers, int * out) {
+    return guarded([&] {
+        if (n_layers < 1 || n_layers > SLOTS) throw std::runtime_error("n_layers must be 1..17");
+        Spec s;
+        parse_spec(kv_spec, n_layers, s);
+        for (int i = 0; i < n_layers; i++) {
+            out[i] = s.kb[i];
+            out[n_layers + i] = s.vb[i];
+            out[2 * n_layers + i] = s.kr[i];
+            out[3 * n_layers + i] = s.vr[i];
+        }
+        return 0;
+    });
+}
+
+void * mk_kv_new(const char * kv_spec, int win, int win_all, int n_layers, int n_seq, int ctx, int page, int n_pages) {
+    Store * s = nullptr;
+    try {
+        if (n_layers < 1 || n_layers > SLOTS) throw std::runtime_error("n_layers must be 1..17");
+        if (n_seq < 1 || n_seq > 64) throw std::runtime_error("n_seq must be 1..64");
+        if (ctx < 1) throw std::runtime_error("ctx must be positive");
+        if (win < 0) throw std::runtime_error("negative window");
+        if (page < 0 || page % ATP_) throw std::runtime_error("page must be a multiple of 32 (0: contiguous)");
+        s = new Store();
+        s->n_layers = n_layers;
+        s->n_seq = n_seq;
+        s->ctx = ctx;
+        parse_spec(kv_spec, n_layers, s->spec);
+        const int ctx32 = (ctx + ATP_ - 1) / ATP_ * ATP_;
+        s->page = page ? page : ctx32;
+        s->pt_stride = (ctx + s->page - 1) / s->page;
+        s->n_pages = n_pages > 0 ? n_pages : n_seq * s->pt_stride;
+        s->win = win;
+        s->win_all = win_all;
+        s->kvrc = ring_rows(win);
+        s->ptab.assign((size_t) n_seq * s->pt_stride, 0);
+        for (int q = 0; q < n_seq; q++)
+            for (int i = 0; i < s->pt_stride; i++) s->ptab[(size_t) q * s->pt_stride + i] = (q * s->pt_stride + i) % s->n_pages;
+        s->n.assign(n_seq, 0);
+        s->top.assign(n_seq, 0);
+        s->ptab_dev = static_cast<int *>(s->dalloc(s->ptab.size() * sizeof(int)));
+        HCK(hipMemcpy(s->ptab_dev, s->ptab.data(), s->ptab.size() * sizeof(int), hipMemcpyHostToDevice));
+        StoreLayout & S = s->S;
+        S.ptab = s->ptab_dev;
+        S.pt_stride = s->pt_stride;
+        S.page = s->page;
+        S.n_pages = s->n_pages;
+        S.kvrc = s->kvrc;
+        S.win = win;
+        S.n_seq = n_seq;
+        const size_t rows = (size_t) NKV * s->n_pages * s->page;
+        for (int l = 0; l < n_layers; l++)
+            for (int w = 0; w < 2; w++) {
+                SideLayout & sd = S.side[l][w];
+                sd.bits = (w ? s->spec.vb : s->spec.kb)[l];
+                sd.rot = (w ? s->spec.vr : s->spec.kr)[l];
+                sd.vals = static_cast<uint8_t *>(s->dalloc(rows * row_bytes(sd.bits)));
+                sd.scs = static_cast<uint16_t *>(s->dalloc(rows * 16));
+                if (s->kvrc > 0 && (sd.bits != 8 || win_all)) {
+                    const size_t rr = (size_t) n_seq * NKV * s->kvrc;
+                    sd.ring = static_cast<int8_t *>(s->dalloc(rr * HD));
+                    sd.rsc = static_cast<uint16_t *>(s->dalloc(rr * 16));
+                    s->ring_bytes += rr * (HD + 16);
+                }
+            }
+        return s;
+    } catch (const std::exception & e) {
+        g_err = e.what();
+        delete s;
+        return nullptr;
+    }
+}
+
+void mk_free(void * h) { delete static_cast<Store *>(h); }
+
+int mk_kv_set_pages(void * h, int seq, const int * pages, int n) {
+    return guarded([&] {
+        Store & s = *as_store(h);
+        check_seq(s, seq);
+        if (n < 0 || n > s.pt_stride) throw std::runtime_error("page table longer than ceil(ctx / page)");
+        for (int i = 0; i < n; i++)
+            if (pages[i] < 0 || pages[i] >= s.n_pages) throw std::runtime_error("physical page " + std::to_string(pages[i]) + " outside the pool");
+        for (int i = 0; i < n; i++) s.ptab[(size_t) seq * s.pt_stride + i] = pages[i];
+        HCK(hipMemcpy(s.ptab_dev + (size_t) seq * s.pt_stride, s.ptab.data() + (size_t) seq * s.pt_stride, (size_t) s.pt_stride * sizeof(int),
+                      hipMemcpyHostToDevice));
+        return 0;
+    });
+}
+
+int mk_kv_append(void * h, int seq, int layer0, int n_layers, int pos, int T, const void * k, const void * v, int dtype, void * stream) {
+    return guarded([&] {
+        Store & s = *as_store(h);
+        check_seq(s, seq);
+        check_layers(s, layer0, n_layers);
+        if (T < 1 || pos < 0 || pos + T > s.ctx) throw std::runtime_error("positions outside 0 .. ctx-1");
+        if (dtype != 0 && dtype != 1) throw std::runtime_error("dtype: 0 fp32, 1 fp16");
+        if (!k || !v) throw std::runtime_error("null K/V pointer");
+        Store::EvSet * es = prof_set(s, 2);
+        prof_mark(es, 0, static_cast<hipStream_t>(stream));
+        HCK(launch_append(s.S, seq, layer0, n_layers, pos, T, k, v, dtype, static_cast<hipStream_t>(stream)));
+        prof_mark(es, 1, static_cast<hipStream_t>(stream));
+        s.top[seq] = std::max(s.top[seq], pos + T);
+        s.n[seq] = std::max(s.n[seq], pos + T);
+        return 0;
+    });
+}
+
+int mk_kv_attend(void * h, int layer0, int n_layers, int n_seq, const int * seqs, const int * lens, int T, const float * q, float * out,
+                 void * stream) {
+    return guarded([&] {
+        Store & s = *as_store(h);
+        check_layers(s, layer0, n_layers);
+        if (T < 1 || T > MAXT) throw std::runtime_error("T must be 1..8");
+        if (n_seq < 1 || n_seq > MAX_SEQ) throw std::runtime_error("1..8 sequences per attend call");
+        if (!q || !out) throw std::runtime_error("null q/out pointer");
+        hipStream_t st = static_cast<hipStream_t>(stream);
+        AttnArgs a{};
+        a.S = s.S;
+        a.T = T;
+        a.R = GQA * T;
+        a.RP = (a.R + 15) / 16 * 16;
+        a.nseq = n_seq;
+        int seg_total = 0;
+        for (int i = 0; i < n_seq; i++) {
+            check_seq(s, seqs[i]);
+            const int L = lens[i];
+            if (L < T || L > s.ctx) throw std::runtime_error("context length " + std::to_string(L) + " outside T .. ctx");
+            const int ws = window_start(L, s.win);
+            if (ws != window_start(L - T + 1, s.win))
+                throw std::runtime_error("the T rows straddle a 640-position window bucket (cap T with mk_kv_cap_T)");
+            SeqDesc & d = a.sd[i];
+            d.seq = seqs[i];
+            d.L = L;
+            d.ws = ws;
+            d.nseg = (L + SEG - 1) / SEG;
+            seg_total += d.nseg;
+        }
+        unsigned rot = 0, rotv = 0;
+        for (int l = 0; l < s.n_layers; l++) {
+            rot |= (unsigned) s.spec.kr[l] << l;
+            rotv |= (unsigned) s.spec.vr[l] << l;
+        }
+        // workspace: prepared queries for all layers; partials for one format group at a time
+        s.grow(s.qh, s.qh_bytes, (size_t) n_layers * n_seq * NKV * a.RP * HD * sizeof(_Float16));
+        const size_t max_items = (size_t) n_layers * NKV * seg_total;
+        s.grow(s.part, s.part_bytes, max_items * a.R * HD * sizeof(float));
+        s.grow(s.ml, s.ml_bytes, max_items * a.R * sizeof(float2));
+        Store::EvSet * es = prof_set(s, 1);
+        prof_mark(es, 0, st);
+        HCK(launch_qprep(q, static_cast<_Float16 *>(s.qh), layer0, n_layers, n_seq, T, a.R, a.RP, rot, st));
+        prof_mark(es, 1, st);
+        // attention launches first, then the combines (the partials of every format group are kept)
+        std::vector<AttnArgs> groups;
+        size_t item_base = 0;
+        for (int l = 0; l < n_layers;) { // consecutive layers with the same K/V bits share one launch
+            const int kb = s.S.side[layer0 + l][0].bits, vb = s.S.side[layer0 + l][1].bits;
+            int e = l + 1;
+            while (e < n_layers && s.S.side[layer0 + e][0].bits == kb && s.S.side[layer0 + e][1].bits == vb) e++;
+            AttnArgs b = a;
+            b.layer0 = layer0 + l;
+            b.nl = e - l;
+            int item = 0;
+            for (int i = 0; i < n_seq; i++) {
+                b.sd[i].item0 = item;
+                item += b.nl * NKV * b.sd[i].nseg;
+            }
+            b.n_items = item;
+            b.qh = static_cast<const _Float16 *>(s.qh) + (size_t) l * n_seq * NKV * a.RP * HD;
+            b.part = static_cast<float *>(s.part) + item_base * a.R * HD;
+            b.ml = static_cast<float2 *>(s.ml) + item_base * a.R;
+            item_base += (size_t) item;
+            HCK(launch_attn(b, kb, vb, s.max_blocks, st));
+            groups.push_back(b);
+            l = e;
+        }
+        prof_mark(es, 2, st);
+        for (const AttnArgs & b : groups) HCK(launch_combine(b, rotv, out + (size_t) (b.layer0 - layer0) * n_seq * T * NH * HD, st));
+        prof_mark(es, 3, st);
+        return 0;
+    });
+}
+
+int mk_kv_rewind(void * h, int seq, int pos) {
+    return guarded([&] { return rewind_seq(*as_store(h), seq, pos); });
+}
+int mk_truncate(void * h, int len) { return mk_kv_rewind(h, 0, len); }
+int mk_rewind_to(void * h, int pos) { return mk_kv_rewind(h, 0, pos); }
+
+void mk_kv_sizes(void * h, long long * per_token, long long * rings, long long * state, long long * checkpoint) {
+    const Store * s = static_cast<const Store *>(h);
+    long long t = 0;
+    if (s)
+        for (int l = 0; l < s->n_layers; l++)
+            for (int w = 0; w < 2; w++) t += (long long) NKV * (row_bytes(s->S.side[l][w].bits) + 16); // host_store.cu:114-120
+    if (per_token) *per_token = t;
+    if (rings) *rings = s ? (long long) s->ring_bytes : 0;
+    if (state) *state = 0;
+    if (checkpoint) *checkpoint = 0;
+}
+
+int mk_kv_state_digest(void * h, int seq, unsigned long long * out, int cap) {
+    return guarded([&] { return digest_seq(*as_store(h), seq, out, cap); });
+}
+int mk_state_digest(void * h, unsigned long long * out, int cap) { return mk_kv_state_digest(h, 0, out, cap); }
+
+int mk_kv_read_rows(void * h, int seq, int layer, int w, int g, int p0, int n, int ring, void * vals, unsigned short * scales) {
+    return guarded([&] {
+        Store & s = *as_store(h);
+        check_seq(s, seq);
+        check_layers(s, layer, 1);
+        if (w < 0 || w > 1 || g < 0 || g >= NKV) throw std::runtime_error("side / kv head out of range");
+        if (p0 < 0 || n < 0 || p0 + n > s.ctx) throw std::runtime_error("rows outside 0 .. ctx-1");
+        const SideLayout & sd = s.S.side[layer][w];
+        HCK(hipDeviceSynchronize());
+        if (ring) {
+            if (!sd.ring) throw std::runtime_error("this side has no window ring");
+            for (int i = 0; i < n; i++) {
+                const size_t r = (size_t) (seq * NKV + g) * s.kvrc + (p0 + i) % s.kvrc;
+                if (vals) HCK(hipMemcpy(static_cast<uint8_t *>(vals) + (size_t) i * HD, sd.ring + r * HD, HD, hipMemcpyDeviceToHost));
+                if (scales) HCK(hipMemcpy(scales + (size_t) i * 8, sd.rsc + r * 8, 16, hipMemcpyDeviceToHost));
+            }
+            return HD;
+        }
+        const size_t rb = (size_t) row_bytes(sd.bits);
+        for (int p = p0; p < p0 + n;) {
+            const int cnt = std::min(p0 + n - p, s.page - p % s.page);
+            const size_t r = s.main_row(seq, g, p);
+            if (vals) HCK(hipMemcpy(static_cast<uint8_t *>(vals) + (size_t) (p - p0) * rb, sd.vals + r * rb, (size_t) cnt * rb, hipMemcpyDeviceToHost));
+            if (scales) HCK(hipMemcpy(scales + (size_t) (p - p0) * 8, sd.scs + r * 8, (size_t) cnt * 16, hipMemcpyDeviceToHost));
+            p += cnt;
+        }
+        return (int) rb;
+    });
+}
+
+int mk_kv_profile(void * h, int enable, double * out, int cap) {
+    return guarded([&] {
+        Store & s = *as_store(h);
+        if (s.prof)
+            for (Store::EvSet & es : s.evs) prof_read(s, es);
+        if (enable) {
+            if (s.evs.empty()) {
+                s.evs.resize(Store::NEV);
+                for (Store::EvSet & es : s.evs)
+                    for (hipEvent_t & e : es.e) HCK(hipEventCreate(&e));
+            }
+            for (double & x : s.prof_acc) x = 0;
+            s.ev_next = 0;
+        }
+        const int n = std::min(cap, 5);
+        for (int i = 0; i < n; i++) out[i] = s.prof_acc[i];
+        s.prof = enable;
+        return n;
+    });
+}
+
+int mk_kv_config(void * h, const char * key, long long value) {
+    return guarded([&] {
+        Store & s = *as_store(h);
+        if (!key) throw std::runtime_error("null key");
+        if (!strcmp(key, "max_blocks")) {
+            if (value < 0) throw std::runtime_error("max_blocks must be >= 0");
+            s.max_blocks = (int) value;
+            return 0;
+        }
+        throw std::runtime_error(std::string("unknown knob ") + key);
+    });
+}
+
+} // extern "C"

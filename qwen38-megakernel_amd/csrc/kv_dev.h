@@ -1,0 +1,151 @@
+// Device-side building blocks of the quantized KV path for gfx950 (CDNA4, wave64).
+//
+// Row formats (one row = 256 values of one (layer, kv head, position, K or V)); both are the reference's
+// (qwen38_mk.cu:2003-2097) so that stored bytes are bit-identical:
+//   q8 : 256 int8 codes in natural order, one fp16 scale per 32 values (am / 127).
+//   b-bit, b = 4..7 : bytes 0..127 = low nibbles (word w = values 8w..8w+7: values 0..3 in the low nibbles of bytes
+//        0..3, values 4..7 in the high nibbles); bytes 128 + w (b-4) .. = the high bits, value k at bit (b-4) k of
+//        that little-endian field; code n = q + 2^(b-1); one fp16 scale d = (signed max) / -2^(b-1) per 32 values.
+// Scales live in a separate [row][8] fp16 array.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include "kv_layout.h"
+
+namespace qkv {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
+
+__device__ __forceinline__ float shfl_xor(float v, int m) { return __shfl_xor(v, m, 64); }
+__device__ __forceinline__ unsigned shfl_xor_u(unsigned v, int m) { return (unsigned) __shfl_xor((int) v, m, 64); }
+
+// ------------------------------------------------------------------------------------------------ quantizers
+// One row per wave: lane l holds values 4l .. 4l+3 (a 32-value block = 8 lanes).
+
+// 256-point FWHT, stage order over index bits 0..7 ascending, butterfly (a+b, a-b), then * 1/16 (qwen38_mk.cu:2048-2068).
+// Index i = 4 lane + k: bits 0..1 in-lane, bits 2..7 = lane bits 0..5.
+__device__ __forceinline__ void fwht256_w64(float (&v)[4]) {
+#pragma unroll
+    for (int m = 1; m < 4; m <<= 1)
+#pragma unroll
+        for (int k = 0; k < 4; k++)
+            if (!(k & m)) {
+                const float a = v[k], b = v[k | m];
+                v[k] = a + b;
+                v[k | m] = a - b;
+            }
+    const int lane = lane_id();
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1)
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const float o = shfl_xor(v[k], m);
+            v[k] = (lane & m) ? o - v[k] : v[k] + o;
+        }
+#pragma unroll
+    for (int k = 0; k < 4; k++) v[k] *= 0.0625f;
+}
+
+// float -> int32 by the hardware conversion: truncates, saturates, NaN -> 0 (the reference's cvt.rzi; a C cast leaves
+// out-of-range and NaN undefined, so the instruction is named explicitly)
+__device__ __forceinline__ int f2i_rz(float x) {
+    int r;
+    asm("v_cvt_i32_f32 %0, %1" : "=v"(r) : "v"(x));
+    return r;
+}
+// round half to even, then convert (__float2int_rn)
+__device__ __forceinline__ int f2i_rn(float x) { return f2i_rz(__builtin_rintf(x)); }
+
+__device__ __forceinline__ uint16_t f2h_bits(float x) {
+    const _Float16 h = (_Float16) x;
+    return __builtin_bit_cast(uint16_t, h);
+}
+__device__ __forceinline__ float h2f_bits(uint16_t b) { return (float) __builtin_bit_cast(_Float16, b); }
+
+// q8_0 store of one row (kv_store_q8, qwen38_mk.cu:2005-2022): codes of this lane's 4 values as one word, scale of its block
+__device__ __forceinline__ unsigned quant_q8(const float (&v)[4], uint16_t & sc) {
+    float am = 0.f;
+#pragma unroll
+    for (int k = 0; k < 4; k++) am = fmaxf(am, fabsf(v[k]));
+    am = fmaxf(am, shfl_xor(am, 1));
+    am = fmaxf(am, shfl_xor(am, 2));
+    am = fmaxf(am, shfl_xor(am, 4));
+    const float id = am > 0.f ? 127.0f / am : 0.f;
+    unsigned w = 0;
+#pragma unroll
+    for (int k = 0; k < 4; k++) w |= ((unsigned) f2i_rn(v[k] * id) & 0xffu) << (8 * k);
+    sc = f2h_bits(am / 127.0f);
+    return w;
+}
+
+// b-bit store (kv_store_q4 :2029-2046 / kv_store_qn :2075-2097): signed max (ties -> larger value), d = sv / -h,
+// id = 1/d, n = min(2h-1, (int) fma(v, id, h + 0.5)).  Returns the 4 codes n (one per byte).
+__device__ __forceinline__ unsigned quant_qn(const float (&v)[4], int bits, uint16_t & sc) {
+    const int h = 1 << (bits - 1);
+    float am = 0.f, sv = 0.f;
+#pragma unroll
+    for (int k = 0; k < 4; k++)
+        if (fabsf(v[k]) > am || (fabsf(v[k]) == am && v[k] > sv)) { am = fabsf(v[k]); sv = v[k]; }
+#pragma unroll
+    for (int m = 1; m <= 4; m <<= 1) {
+        const float oa = shfl_xor(am, m), os = shfl_xor(sv, m);
+        if (oa > am || (oa == am && os > sv)) { am = oa; sv = os; }
+    }
+    const float d = sv / (float) -h, id = d != 0.f ? 1.0f / d : 0.f;
+    unsigned codes = 0;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const int n = min(2 * h - 1, f2i_rz(__builtin_fmaf(v[k], id, (float) h + 0.5f)));
+        codes |= ((unsigned) n & 0xffu) << (8 * k);
+    }
+    sc = f2h_bits(d);
+    return codes;
+}
+
+// ------------------------------------------------------------------------------------------------ dequantization
+// fp16 operands are built with the 0x6400 magic: the half with bits 0x6400 | n is 1024 + n exactly (n < 1024), so
+// (0x6400 | n) - (1024 + bias) is the integer code exactly and one fp16 multiply by the scale rounds d * q once,
+// the same value as the reference's half_rn(d * (float) q) (q8_to_f16 :2336, qn_to_f16 :2458).
+
+__device__ __forceinline__ unsigned perm_b32(unsigned hi_src, unsigned lo_src, unsigned sel) {
+    return __builtin_amdgcn_perm(hi_src, lo_src, sel);
+}
+
+__device__ __forceinline__ half2v as_h2(unsigned x) { return __builtin_bit_cast(half2v, x); }
+__device__ __forceinline__ unsigned as_u(half2v x) { return __builtin_bit_cast(unsigned, x); }
+
+// the hb-bit fields 0..3 of x (field k at bit hb k) moved to bits 4 .. 4+hb-1 of byte k
+template <int HB>
+__device__ __forceinline__ unsigned spread4(unsigned x) {
+    if constexpr (HB == 1) return (((x & 0xfu) * 0x00204081u) & 0x01010101u) << 4; // bit k -> bit 8k (copies disjoint)
+    if constexpr (HB == 2) {
+        x = ((x & 0xffu) * 0x10010u) & 0x00f000f0u; // fields 0,1 at bits 4..7, fields 2,3 at 20..23
+        return (x * 0x41u) & 0x30303030u;          // field 1 -> 12..13, field 3 -> 28..29
+    }
+    if constexpr (HB == 3) {
+        x &= 0xfffu;
+        x = (x | (x << 10)) & 0x003f003fu;
+        x = (x | (x << 5)) & 0x07070707u;
+        return x << 4;
+    }
+    return 0u;
+}
+
+// the biased codes n of the 8 values of one nibble word W (+ its high-bit field H): bytes of lo = values 0..3,
+// bytes of hi = values 4..7
+template <int B>
+__device__ __forceinline__ void word_codes(unsigned W, unsigned H, unsigned & lo, unsigned & hi) {
+    constexpr int HB = B - 4;
+    lo = W & 0x0f0f0f0fu;
+    hi = (W >> 4) & 0x0f0f0f0fu;
+    if constexpr (HB > 0) {
+        lo |= spread4<HB>(H);
+        hi |= spread4<HB>(H >> (4 * HB));
+    }
+}
+
+} // namespace qkv

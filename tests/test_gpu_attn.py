@@ -1,0 +1,148 @@
+"""Gather+attention half on the GPU through the C ABI: outputs against the oracle's exact fp64 attention on the same
+fp16 operands (tolerance 2e-3 relative, max-abs), and the invariances the reference relies on or that this build
+adds: T-invariance, split/grid invariance, page-permutation invariance, q8 rings on q8 sides change nothing."""
+import numpy as np
+import pytest
+
+from kvcase import HD, NH, NKV, append_all, expected_attention, rel_err, synth_kv
+
+pytestmark = pytest.mark.gpu
+TOL = 2e-3
+
+
+def run_attend(torch, st, Q, seqs, lens, T, layer0=0, nl=None):
+    """Q [nl][nseq][T][24][256] numpy -> out numpy, same shape."""
+    nl = nl or Q.shape[0]
+    q = torch.from_numpy(np.ascontiguousarray(Q, np.float32)).cuda()
+    out = torch.full_like(q, float("nan"))
+    st.attend(layer0, nl, seqs, lens, T, q.data_ptr(), out.data_ptr())
+    torch.cuda.synchronize()
+    return out.cpu().numpy()
+
+
+def layer_fmt(st, l):
+    return st.kbits[l], st.vbits[l], st.krot[l], st.vrot[l]
+
+
+def check_case(qkv, oracle, torch, spec, win, L, T, nl=1, seed=0, outliers=False, layers_checked=None):
+    rng = np.random.default_rng(seed)
+    K, V = synth_kv(rng, L, nl, outliers)
+    st = qkv.KVStore(spec, win=win, n_layers=nl, ctx=L)
+    append_all(torch, st, 0, K, V, chunks=[4096] * 64)
+    Q = rng.standard_normal((nl, 1, T, NH, HD)).astype(np.float32)
+    out = run_attend(torch, st, Q, [0], [L], T)
+    assert np.isfinite(out).all()
+    ws = qkv.window_start(L, win)
+    for l in (layers_checked if layers_checked is not None else range(nl)):
+        kb, vb, kr, vr = layer_fmt(st, l)
+        ref = expected_attention(oracle, Q[l, 0], K[:, l], V[:, l], T, kr, vr, kb, vb, ws, win > 0 and kb != 8,
+                                 win > 0 and vb != 8)
+        e = rel_err(out[l, 0], ref)
+        assert e <= TOL, (spec, L, T, l, e)
+    return st, out, (K, V, Q)
+
+
+def test_cfg1_q8_4096(qkv, oracle, torch_gpu):
+    """all q8, one layer, 4,096 positions, one query token, seed 0."""
+    check_case(qkv, oracle, torch_gpu, "", 0, 4096, 1, seed=0)
+
+
+@pytest.mark.parametrize("spec", ["K*=5r,V*=6", "K*=5r,V*=5"])
+def test_preset_f_window(qkv, oracle, torch_gpu, spec):
+    """Preset F (BASELINE's K5r/V6 and the reference's K5r/V5) with the 2,048 window: mixed ring/packed tiles."""
+    check_case(qkv, oracle, torch_gpu, spec, 2048, 5000, 1, nl=2, seed=1, outliers=True)
+
+
+@pytest.mark.parametrize("L", [1, 31, 33, 640, 1025, 2047])
+def test_short_and_ragged(qkv, oracle, torch_gpu, L):
+    check_case(qkv, oracle, torch_gpu, "K*=5r,V*=6", 512, L, 1, seed=L)
+
+
+def test_verify_T8_q8(qkv, oracle, torch_gpu):
+    """BASELINE config 4 shape (T = 8, causal among the 8, all q8), at a shorter context, seed 3."""
+    check_case(qkv, oracle, torch_gpu, "", 0, 3000, 8, seed=3)
+
+
+@pytest.mark.parametrize("T", [2, 3, 5, 8])
+def test_verify_mixed(qkv, oracle, torch_gpu, T):
+    L = 3190  # ws = 1280 (mixed ring / packed); rows L-T .. L-1 share one 640-bucket
+    check_case(qkv, oracle, torch_gpu, "K*=5r,V*=6", 1024, L, T, seed=T, outliers=True)
+
+
+def test_rotated_v_and_mixed_layers(qkv, oracle, torch_gpu):
+    check_case(qkv, oracle, torch_gpu, "K0=4r,V0=7r,K1=8,V1=5,K2=6,V2=8r", 640, 2500, 2, nl=3, seed=5)
+
+
+def test_t_invariance(qkv, oracle, torch_gpu):
+    """Token t of a T-row call equals a 1-row call at context n+t+1 (bitwise; bench/dattn_bench.cu:1140-1160)."""
+    torch = torch_gpu
+    L, T = 3190, 8
+    st, out, (K, V, Q) = check_case(qkv, oracle, torch, "K*=5r,V*=6", 1024, L, T, seed=9)
+    for t in range(T):
+        o1 = run_attend(torch, st, Q[:, :, t:t + 1], [0], [L - T + t + 1], 1)
+        assert np.array_equal(o1[:, :, 0], out[:, :, t]), t
+
+
+def test_grid_invariance(qkv, oracle, torch_gpu):
+    """Outputs do not depend on the launch geometry (max_blocks = split count of the grid), bitwise."""
+    torch = torch_gpu
+    st, out, (K, V, Q) = check_case(qkv, oracle, torch, "K*=5r,V*=6", 2048, 7000, 1, nl=2, seed=6)
+    for mb in (1, 3, 17, 64, 1000):
+        st.config("max_blocks", mb)
+        assert np.array_equal(run_attend(torch, st, Q, [0], [7000], 1), out), mb
+    st.config("max_blocks", 0)
+    assert np.array_equal(run_attend(torch, st, Q, [0], [7000], 1), out)
+
+
+def test_ring_on_q8_sides_changes_nothing(qkv, oracle, torch_gpu):
+    """MK_KV_WIN_ALL (loader.cu:1487-1490): q8 rings on q8 sides give byte-identical outputs."""
+    torch = torch_gpu
+    rng = np.random.default_rng(7)
+    L = 5000
+    K, V = synth_kv(rng, L, 1)
+    Q = rng.standard_normal((1, 1, 1, NH, HD)).astype(np.float32)
+    a = qkv.KVStore("", win=1024, win_all=1, n_layers=1, ctx=L)
+    b = qkv.KVStore("", win=0, n_layers=1, ctx=L)
+    append_all(torch, a, 0, K, V)
+    append_all(torch, b, 0, K, V)
+    assert np.array_equal(run_attend(torch, a, Q, [0], [L], 1), run_attend(torch, b, Q, [0], [L], 1))
+
+
+def test_multi_sequence_paged(qkv, oracle, torch_gpu):
+    """Config 5's shape at reduced lengths: several sequences, 256-position pages under a random permutation; each
+    sequence matches the oracle and equals the same data in a contiguous store bit for bit."""
+    torch = torch_gpu
+    rng = np.random.default_rng(8)
+    lens = [700, 2300, 3100]
+    ctx, page = 3328, 256
+    npg = ctx // page
+    st = qkv.KVStore("K*=5r,V*=6", win=1024, n_layers=2, n_seq=3, ctx=ctx, page=page, n_pages=3 * npg)
+    perm = rng.permutation(3 * npg)
+    data = []
+    for s, L in enumerate(lens):
+        st.set_pages(s, perm[s * npg:(s + 1) * npg])
+        K, V = synth_kv(rng, L, 2, outliers=True)
+        append_all(torch, st, s, K, V, chunks=[1000, 1, 1000, 5000])
+        data.append((K, V))
+    Q = rng.standard_normal((2, 3, 1, NH, HD)).astype(np.float32)
+    out = run_attend(torch, st, Q, [0, 1, 2], lens, 1)
+    for s, L in enumerate(lens):
+        K, V = data[s]
+        ws = qkv.window_start(L, 1024)
+        for l in range(2):
+            ref = expected_attention(oracle, Q[l, s], K[:, l], V[:, l], 1, 1, 0, 5, 6, ws, True, True)
+            assert rel_err(out[l, s], ref) <= TOL, (s, l)
+        flat = qkv.KVStore("K*=5r,V*=6", win=1024, n_layers=2, ctx=ctx)
+        append_all(torch, flat, 0, K, V)
+        assert np.array_equal(run_attend(torch, flat, Q[:, s:s + 1], [0], [L], 1)[:, 0], out[:, s]), s
+
+
+def test_attend_errors(qkv, torch_gpu):
+    st = qkv.KVStore("K*=5r,V*=6", win=1024, n_layers=1, ctx=4000)
+    assert qkv.window_start(3201, 1024) != qkv.window_start(3194, 1024)
+    with pytest.raises(qkv.KVError, match="straddle"):
+        st.attend(0, 1, [0], [3201], 8, 1, 1)
+    with pytest.raises(qkv.KVError, match="T must"):
+        st.attend(0, 1, [0], [100], 9, 1, 1)
+    with pytest.raises(qkv.KVError, match="context"):
+        st.attend(0, 1, [0], [4001], 1, 1, 1)

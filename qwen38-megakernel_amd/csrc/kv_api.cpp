@@ -108,8 +108,6 @@ struct Store {
     std::vector<void *> allocs;
     size_t ring_bytes = 0;
     // workspace of attend (grown on demand)
-    void * qh = nullptr;
-    size_t qh_bytes = 0;
     void * part = nullptr;
     size_t part_bytes = 0;
     void * ml = nullptr;
@@ -139,7 +137,6 @@ struct Store {
             for (hipEvent_t e : es.e)
                 if (e) (void) hipEventDestroy(e);
         for (void * p : allocs) (void) hipFree(p);
-        if (qh) (void) hipFree(qh);
         if (part) (void) hipFree(part);
         if (ml) (void) hipFree(ml);
     }
@@ -417,33 +414,28 @@ int mk_kv_attend(void * h, int layer0, int n_layers, int n_seq, const int * seqs
             check_seq(s, seqs[i]);
             const int L = lens[i];
             if (L < T || L > s.ctx) throw std::runtime_error("context length " + std::to_string(L) + " outside T .. ctx");
-            const int ws = window_start(L, s.win);
-            if (ws != window_start(L - T + 1, s.win))
-                throw std::runtime_error("the T rows straddle a 640-position window bucket (cap T with mk_kv_cap_T)");
+            if ((L - T + ATT_BUCKET_) / ATT_BUCKET_ != (L - 1 + ATT_BUCKET_) / ATT_BUCKET_)
+                throw std::runtime_error("the T rows straddle a 640-position bucket (cap T with mk_kv_cap_T)");
             SeqDesc & d = a.sd[i];
             d.seq = seqs[i];
             d.L = L;
-            d.ws = ws;
-            d.nseg = (L + SEG - 1) / SEG;
+            d.ws = window_start(L, s.win);
+            d.cs = seg_len(L);
+            d.nseg = (L + d.cs - 1) / d.cs;
             seg_total += d.nseg;
         }
-        unsigned rot = 0, rotv = 0;
         for (int l = 0; l < s.n_layers; l++) {
-            rot |= (unsigned) s.spec.kr[l] << l;
-            rotv |= (unsigned) s.spec.vr[l] << l;
+            a.krot |= (unsigned) s.spec.kr[l] << l;
+            a.vrot |= (unsigned) s.spec.vr[l] << l;
         }
-        // workspace: prepared queries for all layers; partials for one format group at a time
-        s.grow(s.qh, s.qh_bytes, (size_t) n_layers * n_seq * NKV * a.RP * HD * sizeof(_Float16));
         const size_t max_items = (size_t) n_layers * NKV * seg_total;
-        s.grow(s.part, s.part_bytes, max_items * a.R * HD * sizeof(float));
+        s.grow(s.part, s.part_bytes, max_items * a.R * HD * sizeof(float) * 2); // (second half: experiment timing stamps)
         s.grow(s.ml, s.ml_bytes, max_items * a.R * sizeof(float2));
         Store::EvSet * es = prof_set(s, 1);
         prof_mark(es, 0, st);
-        HCK(launch_qprep(q, static_cast<_Float16 *>(s.qh), layer0, n_layers, n_seq, T, a.R, a.RP, rot, st));
         prof_mark(es, 1, st);
-        // attention launches first, then the combines (the partials of every format group are kept)
-        std::vector<AttnArgs> groups;
         size_t item_base = 0;
+        std::vector<AttnArgs> groups;
         for (int l = 0; l < n_layers;) { // consecutive layers with the same K/V bits share one launch
             const int kb = s.S.side[layer0 + l][0].bits, vb = s.S.side[layer0 + l][1].bits;
             int e = l + 1;
@@ -457,7 +449,8 @@ int mk_kv_attend(void * h, int layer0, int n_layers, int n_seq, const int * seqs
                 item += b.nl * NKV * b.sd[i].nseg;
             }
             b.n_items = item;
-            b.qh = static_cast<const _Float16 *>(s.qh) + (size_t) l * n_seq * NKV * a.RP * HD;
+            b.q = q + (size_t) l * n_seq * T * NH * HD;
+            b.out = out + (size_t) l * n_seq * T * NH * HD;
             b.part = static_cast<float *>(s.part) + item_base * a.R * HD;
             b.ml = static_cast<float2 *>(s.ml) + item_base * a.R;
             item_base += (size_t) item;
@@ -466,7 +459,21 @@ int mk_kv_attend(void * h, int layer0, int n_layers, int n_seq, const int * seqs
             l = e;
         }
         prof_mark(es, 2, st);
-        for (const AttnArgs & b : groups) HCK(launch_combine(b, rotv, out + (size_t) (b.layer0 - layer0) * n_seq * T * NH * HD, st));
+#ifdef QKV_EXPERIMENT_TIMING
+        if (getenv("QKV_TIMING_FILE")) { // experiment builds: per-item clock stamps of this call's first launch group
+            HCK(hipDeviceSynchronize());
+            const AttnArgs & b = groups[0];
+            std::vector<unsigned long long> ts((size_t) b.n_items * 8);
+            HCK(hipMemcpy(ts.data(), reinterpret_cast<unsigned long long *>(b.part) + (size_t) b.n_items * b.R * HD / 2, ts.size() * 8,
+                          hipMemcpyDeviceToHost));
+            FILE * f = fopen(getenv("QKV_TIMING_FILE"), "ab");
+            if (f) {
+                fwrite(ts.data(), 8, ts.size(), f);
+                fclose(f);
+            }
+        }
+#endif
+        for (const AttnArgs & b : groups) HCK(launch_combine(b, st));
         prof_mark(es, 3, st);
         return 0;
     });

@@ -1,11 +1,16 @@
-// Split-K decode attention over the mixed q8-ring / packed KV store (gfx950, wave64, MFMA f16).
+// Split-K decode attention over the mixed q8-ring / packed KV store (gfx950, wave64, MFMA f16), one kernel per call:
+// query preparation, the attention over every segment, and the merge of the segments into the output.
 //
-// Work: one workgroup of 4 waves per (sequence, layer, kv head, canonical segment of SEG positions).  Wave w takes the
-// 32-position tiles w, w+4, .. of the segment and keeps its own online-softmax state; at the end of the segment the 4
-// states are merged in wave order and written as the segment's partial (m, l, O).  The partition is fixed by the
-// positions alone, so the result never depends on the grid, the split count or the number of query tokens.
+// Work: one workgroup of 4 waves per (sequence, layer, kv head, canonical segment).  The segment length depends only on
+// L's 640-position bucket (seg_len), so the partition -- and with it every rounding -- is independent of the grid,
+// the split count and the number of query tokens sharing the bucket.  Wave w takes the 32-position tiles w, w+4, ..
+// of the segment with its own online-softmax state; the 4 states are merged in wave order into the segment's partial
+// (m, l, O); the last segment of each group of 8 to finish merges the group, and the last group merges the head
+// (fixed orders, so which workgroup performs a merge never changes a bit).
 //
-// Per tile and wave, everything stays in registers (no LDS, no barriers):
+// Per tile and wave: the tile's packed rows are copied HBM -> LDS by global_load_lds_dwordx4 into one of two stages
+// (two tiles in flight per wave, 8 per CU), read into registers in MFMA operand layout, and the stage is refilled with
+// the tile after next before the math starts:
 //   S^T = K Q^T   v_mfma_f32_16x16x32_f16, A = 16 positions x 32 dims of K (lane: position l%16, 8 consecutive dims of
 //                 its quarter l/16 of the row), B = Q^T (lane: query row l%16, the same dims).  Two 16-position subtiles.
 //   softmax       lane (row l%16, quarter q) owns S of positions 4q..4q+3 and 16+4q..16+4q+3 of its row: 8 values,
@@ -23,9 +28,13 @@ namespace qkv {
 constexpr float LOG2E = 1.4426950408889634f;
 constexpr unsigned C64 = 0x64646464u;
 
+// main-store row of (seq, g, p) for wave-uniform arguments: the integer division runs on the vector unit, so the page
+// index is made scalar, and the table is read through the constant address space: a scalar load waits on lgkmcnt
+// only, never on the tile copies in flight
 __device__ __forceinline__ size_t attn_main_row(const StoreLayout & S, int seq, int g, int p) {
-    const int lp = p / S.page;
-    const int phys = S.ptab[seq * S.pt_stride + lp];
+    const int lp = __builtin_amdgcn_readfirstlane(p / S.page);
+    typedef const __attribute__((address_space(4))) int * const_int_p; // no kernel writes the table during a launch
+    const int phys = ((const_int_p) S.ptab)[seq * S.pt_stride + lp];
     return (size_t) (g * S.n_pages + phys) * S.page + (p - lp * S.page);
 }
 
@@ -194,47 +203,149 @@ __device__ __forceinline__ void vcodes(const VRaw<B> & v, int j, unsigned (&c)[4
     }
 }
 
+// the code bytes of nibble word w (0, 1) of the lane's 16 dims for position j: c[0] byte b = dim 16 m + 8 w + b,
+// c[1] byte b = dim 16 m + 8 w + 4 + b (biased codes; q8: the signed bytes)
+template <int B>
+__device__ __forceinline__ void vcodes_word(const VRaw<B> & v, int j, int w, unsigned (&c)[2]) {
+    if constexpr (B == 8) {
+        c[0] = v.d[j][2 * w];
+        c[1] = v.d[j][2 * w + 1];
+    } else {
+        constexpr int HB = B - 4;
+        unsigned hw = 0;
+        if constexpr (HB == 1) hw = (v.h[j][0] >> (8 * w)) & 0xffu;
+        else if constexpr (HB == 2) hw = w ? v.h[j][0] >> 16 : v.h[j][0] & 0xffffu;
+        else if constexpr (HB == 3) hw = w ? (v.h[j][0] >> 24) | (v.h[j][1] << 8) : v.h[j][0] & 0xffffffu;
+        word_codes<B>(v.d[j][w], hw, c[0], c[1]);
+    }
+}
+
+// ------------------------------------------------------------------------------------------------ tile staging
+// Tiles move HBM -> LDS with global_load_lds_dwordx4 (16 bytes per lane, 1 KiB per wave instruction, written at
+// M0 + 16 lane), issued from inline assembly so that the waits are explicit: the compiler would otherwise wait for
+// every outstanding copy before the first LDS read.  Nothing else in the tile loop issues vector-memory loads, so
+// `s_waitcnt vmcnt(n)` with n = the copies of the younger tile in flight is exact.  M0 is not allocatable; only
+// these copies set it in this kernel.
+// Stage layout (STAGE_BYTES, one per wave and stage): K rows [32][32 KB], V rows [32][32 VB], K scales [32][8],
+// V scales [32][8] (fp16).  Rows past the end of the context are copies of the last row (finite, masked later).
+__device__ __forceinline__ void dma16(const void * g, unsigned lds) {
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds), "v"(g) : "memory");
+}
+// the same with a scalar base address and a 32-bit per-lane byte offset (no 64-bit vector address per copy)
+__device__ __forceinline__ void dma16s(const void * base, unsigned voff, unsigned lds) {
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds), "v"(voff), "s"(base) : "memory");
+}
+__device__ __forceinline__ void lds_drain() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+template <int N>
+__device__ __forceinline__ void vm_wait() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+struct TileSrc {
+    const uint8_t * k;
+    const uint16_t * ks;
+    const uint8_t * v;
+    const uint16_t * vs;
+};
+
+// copies of one tile into the stage at LDS address `lds`; returns the number of copy instructions (KB + VB + 1).
+// Full tiles copy contiguous bytes (one address add per instruction); the last, partial tile of a context clamps each
+// 16-byte chunk to the last valid row.
+template <int KB, int VB>
+__device__ __forceinline__ int issue_tile(const TileSrc & t, int nv, unsigned lds, int lane) {
+    constexpr int KR = 2 * KB, VR = 2 * VB; // 16-byte chunks per row
+    if (nv == ATP) {
+        const unsigned off = 16 * lane;
+#pragma unroll
+        for (int j = 0; j < KB; j++) dma16s(t.k + 1024 * j, off, lds + 1024 * j);
+#pragma unroll
+        for (int j = 0; j < VB; j++) dma16s(t.v + 1024 * j, off, lds + 1024 * (KB + j));
+    } else {
+#pragma unroll
+        for (int j = 0; j < KB; j++) {
+            int c = j * 64 + lane;
+            const int r = c / KR;
+            if (r >= nv) c = (nv - 1) * KR + (c - r * KR);
+            dma16(t.k + 16 * c, lds + 1024 * j);
+        }
+#pragma unroll
+        for (int j = 0; j < VB; j++) {
+            int c = j * 64 + lane;
+            const int r = c / VR;
+            if (r >= nv) c = (nv - 1) * VR + (c - r * VR);
+            dma16(t.v + 16 * c, lds + 1024 * (KB + j));
+        }
+    }
+    const int r = min(lane & 31, nv - 1);
+    dma16(lane < 32 ? static_cast<const void *>(t.ks + 8 * r) : static_cast<const void *>(t.vs + 8 * r), lds + 1024 * (KB + VB));
+    return KB + VB + 1;
+}
+
+template <int KB, int VB>
+struct RawTile {
+    KSub<KB> k0, k1; // subtile rows n, 16 + n
+    VRaw<VB> v;      // the lane's 8 positions
+};
+
+// the lane's operands of a staged tile into registers (row n = l % 16, quarter q = l / 16): the K subtiles, then,
+// separately, the V positions (read after the scores, so the K and V registers are never live together)
+template <int KB, int VB>
+__device__ __forceinline__ void read_k(RawTile<KB, VB> & r, const uint8_t * st, int n, int q) {
+    const uint8_t * kr = st;
+    const uint16_t * ksc = reinterpret_cast<const uint16_t *>(st + 1024 * (KB + VB));
+    load_ksub<KB>(r.k0, kr + n * 32 * KB, ksc + n * 8, q);
+    load_ksub<KB>(r.k1, kr + (16 + n) * 32 * KB, ksc + (16 + n) * 8, q);
+}
+template <int KB, int VB>
+__device__ __forceinline__ void read_v(RawTile<KB, VB> & r, const uint8_t * st, int n, int q) {
+    const uint8_t * vr = st + 1024 * KB;
+    const uint16_t * vsc = reinterpret_cast<const uint16_t *>(st + 1024 * (KB + VB)) + 8 * ATP;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const int row = j < 4 ? 4 * q + j : 16 + 4 * q + j - 4;
+        load_vpos<VB>(r.v, j, vr + row * 32 * VB, vsc + row * 8, n);
+    }
+}
+
 // ------------------------------------------------------------------------------------------------ the tile
 template <int NR>
 struct WaveState {
     f32x4 acc[NR][16]; // O^T: instruction i, element e -> dim 64 q + 16 e + i of the lane's row
     float m[NR], l[NR];
     int lim[NR];       // last visible position of the lane's row (-1: padding row)
+    int lim_min;       // last position visible to every real row (L - T), wave-uniform
 };
 
-template <int NR, int KB, int VB>
-__device__ __forceinline__ void attend_tile(WaveState<NR> & st, const half8 (&qf)[NR][8], int p0, int nv, const uint8_t * kbase,
-                                            const uint16_t * ksc, const uint8_t * vbase, const uint16_t * vsc) {
-    const int lane = lane_id(), n = lane & 15, q = lane >> 4;
-    constexpr int KRB = 32 * KB, VRB = 32 * VB;
-    // ---- loads: K subtiles (position n and 16 + n) and V (the lane's 8 positions); rows past the end alias the last row
-    KSub<KB> k0, k1;
-    {
-        const int r0 = min(n, nv - 1), r1 = min(16 + n, nv - 1);
-        load_ksub<KB>(k0, kbase + (size_t) r0 * KRB, ksc + r0 * 8, q);
-        load_ksub<KB>(k1, kbase + (size_t) r1 * KRB, ksc + r1 * 8, q);
-    }
-    VRaw<VB> vr;
-#pragma unroll
-    for (int j = 0; j < 8; j++) {
-        const int rr = min((j < 4 ? 4 * q + j : 16 + 4 * q + j - 4), nv - 1);
-        load_vpos<VB>(vr, j, vbase + (size_t) rr * VRB, vsc + rr * 8, n);
-    }
+// query rows in LDS: fp16 [RP][256] with 16-byte chunk c of row r stored at chunk c ^ (r % 16), so the 16 rows one
+// fragment read touches hit 16 different bank groups
+__device__ __forceinline__ int qchunk(int r, int c) { return r * (HD / 8) + (c ^ (r & 15)); }
+
+// the query fragment of row group rg, K step ks for lane (n, q): 8 fp16 dims 64 q + 8 ks .. of row 16 rg + n
+__device__ __forceinline__ half8 qfrag(const half8 * sQ, int rg, int ks, int n, int q) { return sQ[qchunk(16 * rg + n, 8 * q + ks)]; }
+
+// mid(raw) runs between the softmax and P V: it reads the V operands and releases the stage
+template <int NR, int KB, int VB, class Mid>
+__device__ __forceinline__ void compute_tile(WaveState<NR> & st, const half8 * sQ, int p0, RawTile<KB, VB> & raw, Mid mid) {
+    const int lane = lane_id(), q = lane >> 4, n = lane & 15;
     // ---- S^T = K Q^T
     f32x4 s[2][NR];
 #pragma unroll
     for (int rg = 0; rg < NR; rg++) s[0][rg] = s[1][rg] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int ks = 0; ks < 8; ks++) {
-        const half8 a0 = kfrag<KB>(k0, ks);
-        const half8 a1 = kfrag<KB>(k1, ks);
+        const half8 a0 = kfrag<KB>(raw.k0, ks);
+        const half8 a1 = kfrag<KB>(raw.k1, ks);
 #pragma unroll
         for (int rg = 0; rg < NR; rg++) {
-            s[0][rg] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, qf[rg][ks], s[0][rg], 0, 0, 0);
-            s[1][rg] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, qf[rg][ks], s[1][rg], 0, 0, 0);
+            const half8 b = qfrag(sQ, rg, ks, n, q);
+            s[0][rg] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, b, s[0][rg], 0, 0, 0);
+            s[1][rg] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, b, s[1][rg], 0, 0, 0);
         }
     }
-    // ---- online softmax (log2 units); lane: row n of group rg, positions p0 + 4q + e and p0 + 16 + 4q + e
+    // ---- online softmax (log2 units); lane: its row, positions p0 + 4q + e and p0 + 16 + 4q + e.
+    // The running max moves only when a tile's max exceeds it by more than RESCALE_LOG2 (and on the first visible
+    // tile): until then P = exp2(s - m) <= 2^RESCALE_LOG2 (exact in fp16 range) and O, l keep their scale, so most
+    // tiles need no rescale of O.  A function of the data order within the fixed partition only: deterministic.
+    constexpr float RESCALE_LOG2 = 8.f;
     half8 pf[NR];
     bool rescale = false;
     float alpha[NR];
@@ -242,23 +353,25 @@ __device__ __forceinline__ void attend_tile(WaveState<NR> & st, const half8 (&qf
     for (int rg = 0; rg < NR; rg++) {
         float t[8];
         float mx = -INFINITY;
+        const bool full = p0 + ATP - 1 <= st.lim_min; // every position of the tile visible to every row (uniform)
 #pragma unroll
         for (int e = 0; e < 8; e++) {
             const int pos = p0 + (e < 4 ? 4 * q + e : 16 + 4 * q + e - 4);
             const float sv = (e < 4 ? s[0][rg][e] : s[1][rg][e - 4]) * LOG2E;
-            t[e] = pos <= st.lim[rg] ? sv : -INFINITY;
+            t[e] = full || pos <= st.lim[rg] ? sv : -INFINITY;
             mx = fmaxf(mx, t[e]);
         }
         mx = fmaxf(mx, shfl_xor(mx, 16));
         mx = fmaxf(mx, shfl_xor(mx, 32));
-        const float mnew = fmaxf(st.m[rg], mx);
+        const float mold = st.m[rg];
+        const float mnew = mx > mold + RESCALE_LOG2 ? mx : mold; // (mold = -inf: any finite mx)
         float al = 1.f, ps = 0.f;
         float p[8];
         if (mnew != -INFINITY) {
-            al = exp2f(st.m[rg] - mnew);
+            al = mold == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mold - mnew);
 #pragma unroll
             for (int e = 0; e < 8; e++) {
-                p[e] = exp2f(t[e] - mnew);
+                p[e] = __builtin_amdgcn_exp2f(t[e] - mnew);
                 ps += p[e];
             }
         } else {
@@ -270,51 +383,63 @@ __device__ __forceinline__ void attend_tile(WaveState<NR> & st, const half8 (&qf
         st.l[rg] = __builtin_fmaf(st.l[rg], al, ps);
         st.m[rg] = mnew;
         alpha[rg] = al;
-        rescale |= al != 1.f;
+        rescale |= al != 1.f && mold != -INFINITY; // (O is still zero before the first visible tile)
 #pragma unroll
         for (int e = 0; e < 8; e++) pf[rg][e] = (_Float16) p[e];
     }
-    if (__any(rescale)) {
+    if (__any(rescale)) { // alpha == 1 exactly leaves O unchanged: the skip is exact
 #pragma unroll
         for (int rg = 0; rg < NR; rg++)
 #pragma unroll
             for (int i = 0; i < 16; i++) st.acc[rg][i] *= alpha[rg];
     }
+    mid(raw);
     // ---- O^T += V^T P^T, one instruction per dim 16 m + i of the lane
     half2v dv[4];
 #pragma unroll
-    for (int jp = 0; jp < 4; jp++) dv[jp] = as_h2((vr.s[2 * jp] & 0xffffu) | (vr.s[2 * jp + 1] << 16));
-    unsigned c[8][4];
-#pragma unroll
-    for (int j = 0; j < 8; j++) vcodes<VB>(vr, j, c[j]);
+    for (int jp = 0; jp < 4; jp++) dv[jp] = as_h2((raw.v.s[2 * jp] & 0xffffu) | (raw.v.s[2 * jp + 1] << 16));
     constexpr unsigned XMAG = VB == 8 ? 0x64806480u : 0x64006400u;
     constexpr float VBIAS = VB == 8 ? 1152.f : (float) (1024 + (1 << (VB - 1)));
     const half2v vb2 = {(_Float16) -VBIAS, (_Float16) -VBIAS};
 #pragma unroll
-    for (int i = 0; i < 16; i++) {
-        const int a = i >> 2, b = i & 3;
-        const unsigned sel = (unsigned) b | 0x0c00u | ((unsigned) (4 + b) << 16) | 0x0c000000u;
-        half8 va;
+    for (int w = 0; w < 2; w++) { // nibble word w of the lane: dims 16 m + 8 w .. + 7 (two code registers per position)
+        unsigned c[8][2];
 #pragma unroll
-        for (int jp = 0; jp < 4; jp++) {
-            const half2v x = (as_h2(perm_b32(c[2 * jp + 1][a], c[2 * jp][a], sel) ^ XMAG) + vb2) * dv[jp];
-            va[2 * jp] = x[0];
-            va[2 * jp + 1] = x[1];
+        for (int j = 0; j < 8; j++) vcodes_word<VB>(raw.v, j, w, c[j]);
+#pragma unroll
+        for (int i8 = 0; i8 < 8; i8++) {
+            const int i = 8 * w + i8, a2 = i8 >> 2, b = i8 & 3;
+            const unsigned sel = (unsigned) b | 0x0c00u | ((unsigned) (4 + b) << 16) | 0x0c000000u;
+            half8 va;
+#pragma unroll
+            for (int jp = 0; jp < 4; jp++) {
+                const half2v x = (as_h2(perm_b32(c[2 * jp + 1][a2], c[2 * jp][a2], sel) ^ XMAG) + vb2) * dv[jp];
+                va[2 * jp] = x[0];
+                va[2 * jp + 1] = x[1];
+            }
+#pragma unroll
+            for (int rg = 0; rg < NR; rg++) st.acc[rg][i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pf[rg], st.acc[rg][i], 0, 0, 0);
         }
-#pragma unroll
-        for (int rg = 0; rg < NR; rg++) st.acc[rg][i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pf[rg], st.acc[rg][i], 0, 0, 0);
     }
 }
 
 // ------------------------------------------------------------------------------------------------ the kernel
 template <int NR, int KB, int VB>
-__global__ __launch_bounds__(256) void k_attn(AttnArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NR == 1 ? 2 : 1, NR == 1 ? 2 : 1))) void k_attn(AttnArgs a) {
     constexpr int RP = 16 * NR;
-    __shared__ float s_o[RP][HD + 4];
-    __shared__ float s_m[AWAVES][RP], s_l[AWAVES][RP];
-    const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63, n = lane & 15, q = lane >> 4;
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    // the wave index as a scalar: tile positions, page lookups and source selection stay scalar (SMEM loads, uniform
+    // branches); vector loads there would need vmcnt waits that also drain the tile copies in flight
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63, n = lane & 15, q = lane >> 4;
     const StoreLayout & S = a.S;
+    const unsigned lds0 = (unsigned) (size_t) (__attribute__((address_space(3))) uint8_t *) smem;
+    const unsigned st_lds = (unsigned) __builtin_amdgcn_readfirstlane(lds0 + wv * STAGE_BYTES);
+    half8 * const sQ = reinterpret_cast<half8 *>(smem + ATTN_LDS); // [RP][256] fp16, chunk-swizzled (qchunk)
     for (int item = blockIdx.x; item < a.n_items; item += gridDim.x) {
+#ifdef QKV_EXPERIMENT_TIMING
+        unsigned long long * tstamp = reinterpret_cast<unsigned long long *>(a.part) + (size_t) a.n_items * a.R * HD / 2 + (size_t) item * 8;
+        if (threadIdx.x == 0) tstamp[0] = __builtin_amdgcn_s_memrealtime();
+#endif
         int si = 0;
 #pragma unroll
         for (int i = 1; i < 8; i++)
@@ -323,20 +448,54 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs a) {
         const int local = item - sd.item0;
         const int seg = local % sd.nseg, lg = local / sd.nseg;
         const int g = lg % NKV, l = lg / NKV;
-        const int L = sd.L, ws = sd.ws, seq = sd.seq;
-        const int c0 = seg * SEG, c1 = min(L, c0 + SEG);
+        const int L = sd.L, ws = sd.ws, seq = sd.seq, T = a.T;
+        const int c0 = seg * sd.cs, c1 = min(L, c0 + sd.cs);
         const int ntiles = (c1 - c0 + ATP - 1) / ATP;
+        const int my = ntiles > wv ? (ntiles - wv + AWAVES - 1) / AWAVES : 0; // tiles wv, wv+4, ..
         const SideLayout & SK = S.side[a.layer0 + l][0];
         const SideLayout & SV = S.side[a.layer0 + l][1];
+        const size_t ring0 = (size_t) (seq * NKV + g) * S.kvrc;
 
-        half8 qf[NR][8];
-        {
-            const _Float16 * qb = a.qh + ((size_t) ((l * a.nseq + si) * NKV + g) * RP) * HD;
-#pragma unroll
-            for (int rg = 0; rg < NR; rg++)
-#pragma unroll
-                for (int ks = 0; ks < 8; ks++)
-                    qf[rg][ks] = *reinterpret_cast<const half8 *>(qb + (size_t) (16 * rg + n) * HD + 64 * q + 8 * ks);
+        auto issue = [&](int i) {
+            const int p0 = c0 + ATP * (wv + AWAVES * i), nv = min(ATP, L - p0);
+            const bool ring = S.kvrc > 0 && p0 >= ws; // the window: q8 rows (ring, or the main store of q8 sides)
+            TileSrc t;
+            size_t mr = 0;
+            if (!ring || !SK.ring || !SV.ring) mr = attn_main_row(S, seq, g, p0);
+            const size_t rr = ring ? ring0 + __builtin_amdgcn_readfirstlane(p0 % max(S.kvrc, 1)) : 0;
+            if (ring && SK.ring) {
+                t.k = reinterpret_cast<const uint8_t *>(SK.ring) + rr * HD;
+                t.ks = SK.rsc + rr * 8;
+            } else {
+                t.k = SK.vals + mr * (ring ? HD : 32 * KB);
+                t.ks = SK.scs + mr * 8;
+            }
+            if (ring && SV.ring) {
+                t.v = reinterpret_cast<const uint8_t *>(SV.ring) + rr * HD;
+                t.vs = SV.rsc + rr * 8;
+            } else {
+                t.v = SV.vals + mr * (ring ? HD : 32 * VB);
+                t.vs = SV.scs + mr * 8;
+            }
+            if (ring) issue_tile<8, 8>(t, nv, st_lds, lane);
+            else issue_tile<KB, VB>(t, nv, st_lds, lane);
+        };
+
+        if (my > 0) issue(0);
+        // ---- queries: FWHT when K is stored rotated, * 1/16, fp16 (qwen38_mk.cu:2873-2880), rows r = hh T + t
+        for (int r = wv; r < RP; r += AWAVES) {
+            half2v o0 = {(_Float16) 0.f, (_Float16) 0.f}, o1 = o0;
+            if (r < a.R) {
+                const int hh = r / T, t = r % T;
+                const float4 x = *reinterpret_cast<const float4 *>(a.q + (((size_t) (l * a.nseq + si) * T + t) * NH + GQA * g + hh) * HD + 4 * lane);
+                float v[4] = {x.x, x.y, x.z, x.w};
+                if ((a.krot >> (a.layer0 + l)) & 1u) fwht256_w64(v);
+                o0[0] = (_Float16) (v[0] * 0.0625f);
+                o0[1] = (_Float16) (v[1] * 0.0625f);
+                o1[0] = (_Float16) (v[2] * 0.0625f);
+                o1[1] = (_Float16) (v[3] * 0.0625f);
+            }
+            reinterpret_cast<uint2 *>(sQ + qchunk(r, lane >> 1))[lane & 1] = make_uint2(as_u(o0), as_u(o1));
         }
         WaveState<NR> st;
 #pragma unroll
@@ -344,90 +503,186 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs a) {
             st.m[rg] = -INFINITY;
             st.l[rg] = 0.f;
             const int row = 16 * rg + n;
-            st.lim[rg] = row < a.R ? L - a.T + row % a.T : -1;
+            st.lim[rg] = row < a.R ? L - T + row % T : -1;
 #pragma unroll
             for (int i = 0; i < 16; i++) st.acc[rg][i] = f32x4{0.f, 0.f, 0.f, 0.f};
         }
-        for (int tt = wv; tt < ntiles; tt += AWAVES) {
-            const int p0 = c0 + ATP * tt, nv = min(ATP, L - p0);
-            if (S.kvrc > 0 && p0 >= ws) { // the window: q8 rows from the rings (sides without one are q8 in the main store)
-                const int rr = p0 % S.kvrc;
-                const uint8_t *kb, *vb;
-                const uint16_t *ks, *vs;
-                if (SK.ring) {
-                    const size_t r = (size_t) (seq * NKV + g) * S.kvrc + rr;
-                    kb = reinterpret_cast<const uint8_t *>(SK.ring) + r * HD;
-                    ks = SK.rsc + r * 8;
-                } else {
-                    const size_t r = attn_main_row(S, seq, g, p0);
-                    kb = SK.vals + r * HD;
-                    ks = SK.scs + r * 8;
-                }
-                if (SV.ring) {
-                    const size_t r = (size_t) (seq * NKV + g) * S.kvrc + rr;
-                    vb = reinterpret_cast<const uint8_t *>(SV.ring) + r * HD;
-                    vs = SV.rsc + r * 8;
-                } else {
-                    const size_t r = attn_main_row(S, seq, g, p0);
-                    vb = SV.vals + r * HD;
-                    vs = SV.scs + r * 8;
-                }
-                attend_tile<NR, 8, 8>(st, qf, p0, nv, kb, ks, vb, vs);
+        st.lim_min = L - T;
+        __syncthreads(); // the query rows are complete
+        const uint8_t * const stp = smem + wv * STAGE_BYTES; // (derived from smem: LDS reads)
+        for (int i = 0; i < my; i++) {
+#ifndef QKV_EXPERIMENT_NOWAIT
+            vm_wait<0>(); // tile i has landed (the wave's only copies in flight)
+#endif
+            const int p0 = c0 + ATP * (wv + AWAVES * i);
+            const bool ring = S.kvrc > 0 && p0 >= ws;
+            // K operands now; V operands after the scores, then the stage is free and the next tile streams in during
+            // this one's P V
+            if (ring) {
+                RawTile<8, 8> raw;
+                read_k<8, 8>(raw, stp, n, q);
+                read_v<8, 8>(raw, stp, n, q);
+                lds_drain();
+                if (i + 1 < my) issue(i + 1);
+#ifndef QKV_EXPERIMENT_NOCOMPUTE
+                compute_tile<NR, 8, 8>(st, sQ, p0, raw, [](RawTile<8, 8> &) {});
+#else
+                st.acc[0][0][0] += __builtin_bit_cast(float, raw.k0.d[0] ^ raw.v.d[7][1]);
+#endif
             } else {
-                const size_t r = attn_main_row(S, seq, g, p0);
-                attend_tile<NR, KB, VB>(st, qf, p0, nv, SK.vals + r * (32 * KB), SK.scs + r * 8, SV.vals + r * (32 * VB), SV.scs + r * 8);
+                RawTile<KB, VB> raw;
+                read_k<KB, VB>(raw, stp, n, q);
+                read_v<KB, VB>(raw, stp, n, q);
+                lds_drain();
+                if (i + 1 < my) issue(i + 1);
+#ifndef QKV_EXPERIMENT_NOCOMPUTE
+                compute_tile<NR, KB, VB>(st, sQ, p0, raw, [](RawTile<KB, VB> &) {});
+#else
+                st.acc[0][0][0] += __builtin_bit_cast(float, raw.k0.d[0] ^ raw.v.d[7][1]);
+#endif
             }
         }
-        // ---- merge the 4 waves in order: M = max m_w, O = sum e_w O_w, l = sum e_w l_w
+        // ---- merge the 4 waves in order: M = max m_w, O = sum e_w O_w, l = sum e_w l_w.  Every wave writes its
+        // scaled O rows to its own LDS buffer (the stages are free), then each thread adds the 4 buffers in wave order.
+#ifdef QKV_EXPERIMENT_TIMING
+        if (lane == 0) tstamp[1 + wv] = __builtin_amdgcn_s_memrealtime();
+#endif
+        constexpr int OLD = HD + 4;                                 // row stride (floats) of a wave's O buffer
+        float * const s_m = reinterpret_cast<float *>(smem + AWAVES * 16 * OLD * 4); // [AWAVES][RP]
+        float * const s_l = s_m + AWAVES * RP;                                        // [AWAVES][RP]
+        static_assert(AWAVES * 16 * OLD * 4 + 2 * AWAVES * 3 * 16 * 4 <= ATTN_LDS, "merge buffers inside the stages");
+        __syncthreads(); // every wave is done with its stage
         if (q == 0) {
 #pragma unroll
             for (int rg = 0; rg < NR; rg++) {
-                s_m[wv][16 * rg + n] = st.m[rg];
-                s_l[wv][16 * rg + n] = st.l[rg];
+                s_m[wv * RP + 16 * rg + n] = st.m[rg];
+                s_l[wv * RP + 16 * rg + n] = st.l[rg];
             }
         }
         __syncthreads();
-        float e[NR];
+        const int R = a.R;
 #pragma unroll
-        for (int rg = 0; rg < NR; rg++) {
-            const int row = 16 * rg + n;
-            const float M = fmaxf(fmaxf(s_m[0][row], s_m[1][row]), fmaxf(s_m[2][row], s_m[3][row]));
-            e[rg] = st.m[rg] == -INFINITY ? 0.f : exp2f(st.m[rg] - M);
-        }
-        for (int w = 0; w < AWAVES; w++) {
-            if (wv == w) {
+        for (int rg = 0; rg < NR; rg++) { // one 16-row group per pass: every wave writes, then all threads add
+            {
+                const int row = 16 * rg + n;
+                const float M = fmaxf(fmaxf(s_m[row], s_m[RP + row]), fmaxf(s_m[2 * RP + row], s_m[3 * RP + row]));
+                const float e = st.m[rg] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(st.m[rg] - M);
+                float * o = reinterpret_cast<float *>(smem) + (wv * 16 + n) * OLD + 64 * q;
 #pragma unroll
-                for (int rg = 0; rg < NR; rg++) {
-                    float * o = &s_o[16 * rg + n][64 * q];
+                for (int ee = 0; ee < 4; ee++)
 #pragma unroll
-                    for (int i = 0; i < 16; i++)
-#pragma unroll
-                        for (int ee = 0; ee < 4; ee++) {
-                            const float x = st.acc[rg][i][ee];
-                            o[16 * ee + i] = w == 0 ? e[rg] * x : __builtin_fmaf(e[rg], x, o[16 * ee + i]);
-                        }
-                }
+                    for (int i4 = 0; i4 < 16; i4 += 4) // dims 64 q + 16 ee + i4 .. + 3
+                        *reinterpret_cast<float4 *>(o + 16 * ee + i4) =
+                            make_float4(e * st.acc[rg][i4][ee], e * st.acc[rg][i4 + 1][ee], e * st.acc[rg][i4 + 2][ee], e * st.acc[rg][i4 + 3][ee]);
             }
             __syncthreads();
+            const int nrow = min(16, R - 16 * rg);
+            for (int idx = threadIdx.x; idx < nrow * (HD / 4); idx += 256) {
+                const int r16 = idx / (HD / 4), c4 = idx % (HD / 4);
+                const float * src = reinterpret_cast<const float *>(smem) + r16 * OLD + 4 * c4;
+                float4 y = *reinterpret_cast<const float4 *>(src);
+#pragma unroll
+                for (int w = 1; w < AWAVES; w++) {
+                    const float4 z = *reinterpret_cast<const float4 *>(src + w * 16 * OLD);
+                    y.x += z.x;
+                    y.y += z.y;
+                    y.z += z.z;
+                    y.w += z.w;
+                }
+                *reinterpret_cast<float4 *>(a.part + ((size_t) item * R + 16 * rg + r16) * HD + 4 * c4) = y;
+            }
+            if (rg + 1 < NR) __syncthreads();
         }
-        float * part = a.part + (size_t) item * a.R * HD;
-        for (int idx = threadIdx.x; idx < a.R * (HD / 4); idx += 256) {
-            const int row = idx / (HD / 4), c4 = idx % (HD / 4);
-            *reinterpret_cast<float4 *>(part + (size_t) row * HD + 4 * c4) = *reinterpret_cast<const float4 *>(&s_o[row][4 * c4]);
-        }
-        if (threadIdx.x < a.R) {
+        if (threadIdx.x < R) {
             const int row = threadIdx.x;
-            const float M = fmaxf(fmaxf(s_m[0][row], s_m[1][row]), fmaxf(s_m[2][row], s_m[3][row]));
+            const float M = fmaxf(fmaxf(s_m[row], s_m[RP + row]), fmaxf(s_m[2 * RP + row], s_m[3 * RP + row]));
             float lsum = 0.f;
 #pragma unroll
             for (int w = 0; w < AWAVES; w++) {
-                const float ew = s_m[w][row] == -INFINITY ? 0.f : exp2f(s_m[w][row] - M);
-                lsum = __builtin_fmaf(ew, s_l[w][row], lsum);
+                const float ew = s_m[w * RP + row] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(s_m[w * RP + row] - M);
+                lsum += ew * s_l[w * RP + row];
             }
-            a.ml[(size_t) item * a.R + row] = make_float2(M, lsum);
+            a.ml[(size_t) item * R + row] = make_float2(M, lsum);
         }
-        __syncthreads(); // s_o / s_m are reused by the next item
+#ifdef QKV_EXPERIMENT_TIMING
+        if (threadIdx.x == 0) { tstamp[5] = __builtin_amdgcn_s_memrealtime(); tstamp[6] = __smid(); tstamp[7] = ntiles; }
+#endif
+        __syncthreads(); // the LDS is reused by the next item
     }
+}
+
+// ------------------------------------------------------------------------------------------------ combine
+// One workgroup per output row (layer, sequence, kv head, row r): the canonical merge of the head's segment partials
+// (attn_combine, qwen38_mk.cu:4617-4700): M = max m (exact, order-free), e_c = exp2(m_c - M) (0 for m = -inf);
+// wave w sums the segments c = w, w+4, .. in order (all its loads issued together), the four sums are added in wave
+// order; y = O / l, then the V un-rotation when V is stored rotated.  The order is fixed by the segment index alone.
+__global__ __launch_bounds__(256) void k_combine(AttnArgs a) {
+    __shared__ float4 s_num[AWAVES][64];
+    __shared__ float s_den[AWAVES];
+    const int R = a.R, T = a.T;
+    int b = blockIdx.x;
+    const int r = b % R;
+    b /= R;
+    const int g = b % NKV;
+    b /= NKV;
+    const int si = b % a.nseq, l = b / a.nseq;
+    const SeqDesc & sd = a.sd[si];
+    const int nseg = sd.nseg;
+    const size_t head0 = (size_t) sd.item0 + (size_t) (l * NKV + g) * nseg;
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    float M = -INFINITY;
+    for (int c = lane; c < nseg; c += 64) M = fmaxf(M, a.ml[(head0 + c) * R + r].x);
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) M = fmaxf(M, shfl_xor(M, o));
+    constexpr int PER = MAX_SEG / AWAVES;
+    float2 ml[PER];
+    float4 o[PER];
+#pragma unroll
+    for (int k = 0; k < PER; k++) {
+        const int c = wv + AWAVES * k;
+        if (c < nseg) {
+            ml[k] = a.ml[(head0 + c) * R + r];
+            o[k] = *reinterpret_cast<const float4 *>(a.part + ((head0 + c) * R + r) * HD + 4 * lane);
+        }
+    }
+    float4 num = make_float4(0.f, 0.f, 0.f, 0.f);
+    float den = 0.f;
+#pragma unroll
+    for (int k = 0; k < PER; k++) {
+        const int c = wv + AWAVES * k;
+        if (c < nseg) {
+            const float e = ml[k].x == -INFINITY ? 0.f : exp2f(ml[k].x - M);
+            num.x = __builtin_fmaf(e, o[k].x, num.x);
+            num.y = __builtin_fmaf(e, o[k].y, num.y);
+            num.z = __builtin_fmaf(e, o[k].z, num.z);
+            num.w = __builtin_fmaf(e, o[k].w, num.w);
+            den = __builtin_fmaf(e, ml[k].y, den);
+        }
+    }
+    s_num[wv][lane] = num;
+    if (lane == 0) s_den[wv] = den;
+    __syncthreads();
+    if (wv != 0) return;
+    float4 y = s_num[0][lane];
+    float dd = s_den[0];
+#pragma unroll
+    for (int k = 1; k < AWAVES; k++) {
+        const float4 z = s_num[k][lane];
+        y.x += z.x;
+        y.y += z.y;
+        y.z += z.z;
+        y.w += z.w;
+        dd += s_den[k];
+    }
+    float v[4] = {y.x / dd, y.y / dd, y.z / dd, y.w / dd};
+    if ((a.vrot >> (a.layer0 + l)) & 1u) fwht256_w64(v);
+    const int h = GQA * g + r / T, t = r % T;
+    *reinterpret_cast<float4 *>(a.out + (((size_t) (l * a.nseq + si) * T + t) * NH + h) * HD + 4 * lane) = make_float4(v[0], v[1], v[2], v[3]);
+}
+
+hipError_t launch_combine(const AttnArgs & a, hipStream_t st) {
+    hipLaunchKernelGGL(k_combine, dim3(a.nl * a.nseq * NKV * a.R), dim3(256), 0, st, a);
+    return hipGetLastError();
 }
 
 // ------------------------------------------------------------------------------------------------ dispatch
@@ -462,9 +717,19 @@ hipError_t launch_attn(const AttnArgs & a, int kb, int vb, int max_blocks, hipSt
     else if (nr == 2) k = pick<2>(kb, vb);
     else if (nr == 3) k = pick<3>(kb, vb);
     if (!k) return hipErrorInvalidValue;
+    static thread_local const void * configured[128];
+    static thread_local int n_configured = 0;
+    bool done = false;
+    for (int i = 0; i < n_configured; i++) done |= configured[i] == (const void *) k;
+    const int lds = ATTN_LDS + a.RP * HD * 2;
+    if (!done) {
+        const hipError_t e = hipFuncSetAttribute((const void *) k, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+        if (e != hipSuccess) return e;
+        if (n_configured < 128) configured[n_configured++] = (const void *) k;
+    }
     int blocks = a.n_items;
     if (max_blocks > 0 && blocks > max_blocks) blocks = max_blocks;
-    hipLaunchKernelGGL(k, dim3(blocks), dim3(256), 0, st, a);
+    hipLaunchKernelGGL(k, dim3(blocks), dim3(256), lds, st, a);
     return hipGetLastError();
 }
 

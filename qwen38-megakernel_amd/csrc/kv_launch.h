@@ -10,29 +10,42 @@ struct SeqDesc {
     int seq;   // store sequence (lane) index
     int L;     // context length after this call's rows: positions 0 .. L-1
     int ws;    // window start: tiles at positions >= ws are read from the q8 ring
-    int nseg;  // canonical segments: ceil(L / SEG)
+    int cs;    // canonical segment length (a function of L's 640-bucket only)
+    int nseg;  // segments: ceil(L / cs) <= 128
     int item0; // first work item of this sequence in the launch
 };
 
 struct AttnArgs {
     StoreLayout S;
-    int layer0;    // first slot of the launch
-    int nl;        // layers in the launch (all with the same K/V bits)
-    int T, R;      // query tokens, query rows per kv head (6 T)
-    int RP;        // padded rows (16 per MFMA row group)
+    int layer0;          // first slot of the launch
+    int nl;              // layers in the launch (all with the same K/V bits)
+    int T, R, RP;        // query tokens, query rows per kv head (6 T), rows padded to 16 per MFMA row group
     int nseq;
-    int n_items;
+    int n_items;         // (sequence, layer, kv head, segment) work items
+    unsigned krot, vrot; // per-slot bit masks: K / V stored rotated
     SeqDesc sd[8];
-    const _Float16 * qh; // [nl][nseq][NKV][RP][256] prepared fp16 queries
-    float * part;        // [item][R][256] per-segment partial outputs (unnormalised)
+    const float * q;     // [nl][nseq][T][NH][HD] queries of this launch's layers (fp32, before the 1/16 scale)
+    float * out;         // [nl][nseq][T][NH][HD]
+    float * part;        // [item][R][HD] per-segment partial outputs (unnormalised)
     float2 * ml;         // [item][R] per-segment (max in log2 units, sum)
 };
+
+// canonical segment length: 32 * max(4, ceil(Lb / 4096)) with Lb = L rounded up to a 640 bucket, so at most 128
+// segments per kv head (one layer's 4 heads fill 2 workgroups on each of the 256 CUs) and the same partition for every
+// row count T whose rows share one bucket
+inline __host__ __device__ int seg_len(int L) {
+    const int lb = (L + ATT_BUCKET - 1) / ATT_BUCKET * ATT_BUCKET;
+    const int u = (lb + 4095) / 4096;
+    return ATP * (u > 4 ? u : 4);
+}
+constexpr int MAX_SEG = 128;
+constexpr int STAGE_BYTES = 2 * 32 * 256 + 1024; // one 32-position tile, widest format (q8 K and V) + its scales
+constexpr int ATTN_LDS = AWAVES * STAGE_BYTES;   // one stage per wave (+ the query rows: RP * 512 bytes)
 
 hipError_t launch_append(const StoreLayout & S, int seq, int layer0, int nl, int pos, int T, const void * k, const void * v, int f16,
                          hipStream_t st);
 hipError_t launch_ring_refill(const StoreLayout & S, int seq, int nl, int p0, int p1, hipStream_t st);
-hipError_t launch_qprep(const float * q, _Float16 * qh, int layer0, int nl, int nseq, int T, int R, int RP, unsigned rotmask, hipStream_t st);
 hipError_t launch_attn(const AttnArgs & a, int kb, int vb, int max_blocks, hipStream_t st);
-hipError_t launch_combine(const AttnArgs & a, unsigned rotv_mask, float * out, hipStream_t st);
+hipError_t launch_combine(const AttnArgs & a, hipStream_t st);
 
 } // namespace qkv

@@ -18,8 +18,6 @@ constexpr int NH = 24;            // query heads (GQA 6)
 constexpr int GQA = NH / NKV;
 constexpr int ATP = 32;           // positions per attention tile
 constexpr int ATT_BUCKET = 640;   // the reference's window / partition bucket (mk_shared.cuh:263-265)
-constexpr int SEG = 1024;         // canonical split-K segment: partials are per segment, never per launch
-constexpr int SEG_TILES = SEG / ATP;
 constexpr int AWAVES = 4;         // waves per attention workgroup (tiles of a segment dealt round-robin)
 constexpr int MAXT = 8;           // query tokens per call (1 + 7 drafts)
 constexpr int MAXR = GQA * MAXT;  // query rows per kv head

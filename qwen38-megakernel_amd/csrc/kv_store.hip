@@ -1,4 +1,4 @@
-// Append/evict half of the KV path, the query preparation and the split-K combine (gfx950, wave64).
+// Append/evict half of the KV path (gfx950, wave64).
 //
 // k_append      : new K/V rows -> optional 256-point FWHT -> main row in the side's format (q8 or 4..7-bit packed)
 //                 and, for sides with a window, the q8 ring copy of the same rotated values (kv_store,
@@ -6,9 +6,6 @@
 //                 rule: the packed row was written from the same fp32 values, so nothing is requantized later.
 // k_ring_refill : after a rewind, ring rows re-stored as q8 of the fp32-dequantized main rows (k_ring_refill,
 //                 qwen38_mk.cu:2485-2517).
-// k_qprep       : query rows -> FWHT when K is stored rotated -> * 1/16 -> fp16 (qwen38_mk.cu:2873-2880).
-// k_combine     : per query row, the canonical-order merge of the segment partials (attn_combine, :4617-4700)
-//                 and the V un-rotation when V is stored rotated.
 #include "kv_dev.h"
 #include "kv_launch.h"
 
@@ -127,86 +124,6 @@ __global__ __launch_bounds__(256) void k_ring_refill(StoreLayout S, int seq, int
     if ((lane & 7) == 0) sd.rsc[rr * 8 + (lane >> 3)] = rs;
 }
 
-// One wave per padded query row: q [nl][nseq][T][NH][256] fp32 -> qh [nl][nseq][NKV][RP][256] fp16.  Row r of kv head g
-// is query head 6g + r / T, token r % T (the reference's row order, qwen38_mk.cu:2866-2870); rows >= R are zero.
-__global__ __launch_bounds__(256) void k_qprep(const float * q, _Float16 * qh, int layer0, int nl, int nseq, int T, int R, int RP,
-                                               unsigned rotmask) {
-    const int wave = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (wave >= nl * nseq * NKV * RP) return;
-    const int lane = threadIdx.x & 63;
-    const int row = wave % RP;
-    int r = wave / RP;
-    const int g = r % NKV;
-    r /= NKV;
-    const int si = r % nseq, l = r / nseq;
-    half2v o0 = {(_Float16) 0.f, (_Float16) 0.f}, o1 = o0;
-    if (row < R) {
-        const int hh = row / T, t = row % T, h = GQA * g + hh;
-        const float4 x = *reinterpret_cast<const float4 *>(q + (((size_t) (l * nseq + si) * T + t) * NH + h) * HD + 4 * lane);
-        float v[4] = {x.x, x.y, x.z, x.w};
-        if ((rotmask >> (layer0 + l)) & 1u) fwht256_w64(v);
-        o0[0] = (_Float16) (v[0] * 0.0625f);
-        o0[1] = (_Float16) (v[1] * 0.0625f);
-        o1[0] = (_Float16) (v[2] * 0.0625f);
-        o1[1] = (_Float16) (v[3] * 0.0625f);
-    }
-    *reinterpret_cast<uint2 *>(qh + (size_t) wave * HD + 4 * lane) = make_uint2(as_u(o0), as_u(o1));
-}
-
-// One workgroup (4 waves) per output row (layer, sequence, token, query head).  Wave w sums the segments c = w, w+4, ..
-// in order; the four sums are then added in wave order.  M (the max) is exact and order-free, so the result depends on
-// the canonical segments only, never on the launch geometry of the attention kernel.
-__global__ __launch_bounds__(256) void k_combine(AttnArgs a, unsigned rotv_mask, float * out) {
-    __shared__ float4 s_num[4][64];
-    __shared__ float s_den[4];
-    const int T = a.T, R = a.R;
-    int b = blockIdx.x;
-    const int h = b % NH;
-    b /= NH;
-    const int t = b % T;
-    b /= T;
-    const int si = b % a.nseq, l = b / a.nseq;
-    const int g = h / GQA, r = (h % GQA) * T + t;
-    const SeqDesc & sd = a.sd[si];
-    const int nseg = sd.nseg;
-    const size_t item0 = (size_t) sd.item0 + (size_t) (l * NKV + g) * nseg;
-    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-    float M = -INFINITY;
-    for (int c = lane; c < nseg; c += 64) M = fmaxf(M, a.ml[(item0 + c) * R + r].x);
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) M = fmaxf(M, shfl_xor(M, o));
-    float4 num = make_float4(0.f, 0.f, 0.f, 0.f);
-    float den = 0.f;
-    for (int c = wv; c < nseg; c += 4) {
-        const float2 ml = a.ml[(item0 + c) * R + r];
-        const float e = ml.x == -INFINITY ? 0.f : exp2f(ml.x - M);
-        const float4 o = *reinterpret_cast<const float4 *>(a.part + ((item0 + c) * R + r) * HD + 4 * lane);
-        num.x = __builtin_fmaf(e, o.x, num.x);
-        num.y = __builtin_fmaf(e, o.y, num.y);
-        num.z = __builtin_fmaf(e, o.z, num.z);
-        num.w = __builtin_fmaf(e, o.w, num.w);
-        den = __builtin_fmaf(e, ml.y, den);
-    }
-    s_num[wv][lane] = num;
-    if (lane == 0) s_den[wv] = den;
-    __syncthreads();
-    if (wv != 0) return;
-    float4 y = s_num[0][lane];
-    float dd = s_den[0];
-#pragma unroll
-    for (int k = 1; k < 4; k++) {
-        const float4 z = s_num[k][lane];
-        y.x += z.x;
-        y.y += z.y;
-        y.z += z.z;
-        y.w += z.w;
-        dd += s_den[k];
-    }
-    float v[4] = {y.x / dd, y.y / dd, y.z / dd, y.w / dd};
-    if ((rotv_mask >> (a.layer0 + l)) & 1u) fwht256_w64(v);
-    *reinterpret_cast<float4 *>(out + (((size_t) (l * a.nseq + si) * T + t) * NH + h) * HD + 4 * lane) = make_float4(v[0], v[1], v[2], v[3]);
-}
-
 hipError_t launch_append(const StoreLayout & S, int seq, int layer0, int nl, int pos, int T, const void * k, const void * v, int f16,
                          hipStream_t st) {
     const int waves = T * nl * NKV * 2;
@@ -219,18 +136,6 @@ hipError_t launch_ring_refill(const StoreLayout & S, int seq, int nl, int p0, in
     if (n <= 0) return hipSuccess;
     const long long waves = (long long) n * nl * NKV * 2;
     hipLaunchKernelGGL(k_ring_refill, dim3((unsigned) ((waves + 3) / 4)), dim3(256), 0, st, S, seq, nl, p0, n);
-    return hipGetLastError();
-}
-
-hipError_t launch_qprep(const float * q, _Float16 * qh, int layer0, int nl, int nseq, int T, int R, int RP, unsigned rotmask, hipStream_t st) {
-    const int waves = nl * nseq * NKV * RP;
-    hipLaunchKernelGGL(k_qprep, dim3((waves + 3) / 4), dim3(256), 0, st, q, qh, layer0, nl, nseq, T, R, RP, rotmask);
-    return hipGetLastError();
-}
-
-hipError_t launch_combine(const AttnArgs & a, unsigned rotv_mask, float * out, hipStream_t st) {
-    const int blocks = a.nl * a.nseq * a.T * NH;
-    hipLaunchKernelGGL(k_combine, dim3(blocks), dim3(256), 0, st, a, rotv_mask, out);
     return hipGetLastError();
 }
 

@@ -9,7 +9,7 @@ import ctypes
 import os
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libqwen38_kv.so")
+LIB_PATH = os.environ.get("QKV_LIB") or os.path.join(HERE, "libqwen38_kv.so")
 
 NKV, NH, HD = 4, 24, 256
 

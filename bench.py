@@ -67,6 +67,21 @@ def timed(torch, fn, steps, warmup):
     return (time.perf_counter() - t0) / steps
 
 
+def profiled(torch, st, fn, steps):
+    """`steps` calls of fn with the store's kernel timing on (after one untimed call); the event totals + wall time."""
+    fn()
+    torch.cuda.synchronize()
+    st.profile(1)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        fn()
+    torch.cuda.synchronize()
+    t = (time.perf_counter() - t0) / steps
+    p = st.profile(0)
+    p["step_s"] = t
+    return p
+
+
 def traffic_from_profiles(name):
     """HBM bytes per launch of the dominant kernel from the committed rocprofv3 --pmc summary, if present."""
     p = os.path.join(ROOT, "profiles", name)
@@ -98,15 +113,14 @@ def bench_cfg3(torch, qkv, steps, warmup):
         st.attend(0, nl, [0], [L], 1, qp, op)
 
     per_layer_bytes = NKV * kv_bytes(L, ws, 5, 6, True)
-    st.profile(1)
+    # step times with profiling off; kernel durations from a second, profiled pass of the same calls (HIP events on the
+    # launch stream around each attention / combine launch; warmup calls excluded)
     t_layers = timed(torch, step_layers, steps, warmup)
-    prof = st.profile(0)
-    # the timed region's kernel durations (HIP events on the launch stream): warmup calls included, same work each
+    prof = profiled(torch, st, step_layers, steps)
     calls = prof["calls"]
     attn_avg = prof["attn_ms"] / calls * 1e-3
-    st.profile(1)
     t_fused = timed(torch, step_fused, steps, warmup)
-    prof_f = st.profile(0)
+    prof_f = profiled(torch, st, step_fused, steps)
     fused_attn_avg = prof_f["attn_ms"] / prof_f["calls"] * 1e-3
     ok = bool(torch.isfinite(out).all().item())
     return {
@@ -114,7 +128,7 @@ def bench_cfg3(torch, qkv, steps, warmup):
         "step_s": t_layers, "positions_per_s": nl * L / t_layers, "gbps": nl * per_layer_bytes / t_layers / 1e9,
         "attn_kernel_avg_s": attn_avg, "attn_kernel_bytes": per_layer_bytes,
         "attn_kernel_gbps": per_layer_bytes / attn_avg / 1e9,
-        "qprep_avg_s": prof["qprep_ms"] / calls * 1e-3, "combine_avg_s": prof["combine_ms"] / calls * 1e-3,
+        "combine_avg_s": prof["combine_ms"] / calls * 1e-3, "profiled_step_s": prof["step_s"],
         "fused16_step_s": t_fused, "fused16_positions_per_s": nl * L / t_fused,
         "fused16_gbps": nl * per_layer_bytes / t_fused / 1e9, "fused16_attn_kernel_avg_s": fused_attn_avg,
         "fused16_attn_kernel_gbps": nl * per_layer_bytes / fused_attn_avg / 1e9, "finite": ok,
@@ -147,13 +161,12 @@ def bench_cfg2(torch, qkv, nsteps=512):
             st.append(0, 0, nl, 8 * s, 8, kp + s * stride, vp + s * stride, 1)
 
     run()  # warm
-    st.profile(1)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     run()
     torch.cuda.synchronize()
     t = (time.perf_counter() - t0) / nsteps
-    prof = st.profile(0)
+    prof = profiled(torch, st, run, 1)
     return {"steps": nsteps, "us_per_step": t * 1e6, "kernel_us_per_step": prof["append_ms"] / nsteps * 1e3,
             "rows_per_step": 8 * nl * NKV * 2}
 
@@ -231,14 +244,25 @@ def main():
     ap.add_argument("--configs", default="1,2,3,4,5")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run 5 plain device copies of MIB MiB (the byte-counter calibration for rocprofv3 --pmc)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only (the KV path shards by kv head / sequence / context with no "
               "collective in this round); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
     import torch
-    import qkv
     torch.cuda.set_device(0)
+    if args.copy_calibration:
+        n = args.copy_calibration << 20
+        src = torch.ones(n, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes": n, "copies": 5}))
+        return
+    import qkv
     cfgs = {int(c) for c in args.configs.split(",") if c}
     extra = {}
     if 3 in cfgs:

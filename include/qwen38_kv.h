@@ -92,8 +92,9 @@ int mk_kv_read_rows(void * h, int seq, int layer, int w, int g, int p0, int n, i
 int mk_kv_config(void * h, const char * key, long long value);
 
 /* Kernel timing with HIP events on the launch stream (the reference's MK_PROFILE per-phase means, engine.cu:382-506).
- * enable = 1 resets and starts recording every attend call's query-prep, attention and combine kernels; 0 stops.
- * out[0..5): calls, then total milliseconds of query prep, attention, combine, append.  Returns the count written. */
+ * enable = 1 resets and starts recording every attend call's attention and combine kernels (the query preparation
+ * runs inside the attention kernel) and every append; 0 stops.
+ * out[0..4): attend calls, then total milliseconds of attention, combine, append.  Returns the count written. */
 int mk_kv_profile(void * h, int enable, double * out, int cap);
 
 /* Host-only geometry and grammar helpers (no GPU needed). */

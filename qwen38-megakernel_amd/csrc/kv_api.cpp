@@ -116,12 +116,12 @@ struct Store {
     // mk_kv_profile: a pool of event sets recorded around each call's kernels on the launch stream; a set's elapsed times
     // are read only when the pool wraps around or profiling stops, so timed back-to-back calls never wait on the host
     struct EvSet {
-        hipEvent_t e[4] = {};
-        int kind = 0; // 0 free, 1 attend (qprep | attention | combine), 2 append
+        hipEvent_t e[3] = {};
+        int kind = 0; // 0 free, 1 attend (attention | combine), 2 append
     };
     static constexpr int NEV = 256;
     int prof = 0;
-    double prof_acc[5] = {0, 0, 0, 0, 0}; // calls, qprep, attention, combine, append (ms)
+    double prof_acc[4] = {0, 0, 0, 0}; // calls, attention, combine, append (ms)
     std::vector<EvSet> evs;
     int ev_next = 0;
 
@@ -159,16 +159,16 @@ void prof_read(Store & s, Store::EvSet & es) {
     if (!es.kind) return;
     float ms = 0.f;
     if (es.kind == 1) {
-        HCK(hipEventSynchronize(es.e[3]));
+        HCK(hipEventSynchronize(es.e[2]));
         s.prof_acc[0] += 1;
-        for (int i = 0; i < 3; i++) {
+        for (int i = 0; i < 2; i++) {
             HCK(hipEventElapsedTime(&ms, es.e[i], es.e[i + 1]));
             s.prof_acc[1 + i] += ms;
         }
     } else {
         HCK(hipEventSynchronize(es.e[1]));
         HCK(hipEventElapsedTime(&ms, es.e[0], es.e[1]));
-        s.prof_acc[4] += ms;
+        s.prof_acc[3] += ms;
     }
     es.kind = 0;
 }
@@ -433,7 +433,6 @@ int mk_kv_attend(void * h, int layer0, int n_layers, int n_seq, const int * seqs
         s.grow(s.ml, s.ml_bytes, max_items * a.R * sizeof(float2));
         Store::EvSet * es = prof_set(s, 1);
         prof_mark(es, 0, st);
-        prof_mark(es, 1, st);
         size_t item_base = 0;
         std::vector<AttnArgs> groups;
         for (int l = 0; l < n_layers;) { // consecutive layers with the same K/V bits share one launch
@@ -458,7 +457,7 @@ int mk_kv_attend(void * h, int layer0, int n_layers, int n_seq, const int * seqs
             groups.push_back(b);
             l = e;
         }
-        prof_mark(es, 2, st);
+        prof_mark(es, 1, st);
 #ifdef QKV_EXPERIMENT_TIMING
         if (getenv("QKV_TIMING_FILE")) { // experiment builds: per-item clock stamps of this call's first launch group
             HCK(hipDeviceSynchronize());
@@ -474,7 +473,7 @@ int mk_kv_attend(void * h, int layer0, int n_layers, int n_seq, const int * seqs
         }
 #endif
         for (const AttnArgs & b : groups) HCK(launch_combine(b, st));
-        prof_mark(es, 3, st);
+        prof_mark(es, 2, st);
         return 0;
     });
 }
@@ -541,12 +540,12 @@ int mk_kv_profile(void * h, int enable, double * out, int cap) {
             if (s.evs.empty()) {
                 s.evs.resize(Store::NEV);
                 for (Store::EvSet & es : s.evs)
-                    for (hipEvent_t & e : es.e) HCK(hipEventCreate(&e));
+                    for (hipEvent_t & e : es.e) HCK(hipEventCreateWithFlags(&e, hipEventDisableSystemFence));
             }
             for (double & x : s.prof_acc) x = 0;
             s.ev_next = 0;
         }
-        const int n = std::min(cap, 5);
+        const int n = std::min(cap, 4);
         for (int i = 0; i < n; i++) out[i] = s.prof_acc[i];
         s.prof = enable;
         return n;

@@ -163,10 +163,10 @@ class KVStore:
         return vals, sc
 
     def profile(self, enable):
-        """Start (1) / stop (0) kernel timing; returns {calls, qprep_ms, attn_ms, combine_ms, append_ms} so far."""
-        out = (ctypes.c_double * 5)()
-        _check(lib().mk_kv_profile(self.h, int(enable), out, 5))
-        return dict(zip(("calls", "qprep_ms", "attn_ms", "combine_ms", "append_ms"), list(out)))
+        """Start (1) / stop (0) kernel timing; returns {calls, attn_ms, combine_ms, append_ms} so far."""
+        out = (ctypes.c_double * 4)()
+        _check(lib().mk_kv_profile(self.h, int(enable), out, 4))
+        return dict(zip(("calls", "attn_ms", "combine_ms", "append_ms"), list(out)))
 
     def config(self, key, value):
         _check(lib().mk_kv_config(self.h, key.encode(), value))

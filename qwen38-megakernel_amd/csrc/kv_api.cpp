@@ -429,7 +429,7 @@ int mk_kv_attend(void * h, int layer0, int n_layers, int n_seq, const int * seqs
             a.vrot |= (unsigned) s.spec.vr[l] << l;
         }
         const size_t max_items = (size_t) n_layers * NKV * seg_total;
-        s.grow(s.part, s.part_bytes, max_items * a.R * HD * sizeof(float) * 2); // (second half: experiment timing stamps)
+        s.grow(s.part, s.part_bytes, max_items * a.R * HD * sizeof(float));
         s.grow(s.ml, s.ml_bytes, max_items * a.R * sizeof(float2));
         Store::EvSet * es = prof_set(s, 1);
         prof_mark(es, 0, st);
@@ -458,20 +458,6 @@ int mk_kv_attend(void * h, int layer0, int n_layers, int n_seq, const int * seqs
             l = e;
         }
         prof_mark(es, 1, st);
-#ifdef QKV_EXPERIMENT_TIMING
-        if (getenv("QKV_TIMING_FILE")) { // experiment builds: per-item clock stamps of this call's first launch group
-            HCK(hipDeviceSynchronize());
-            const AttnArgs & b = groups[0];
-            std::vector<unsigned long long> ts((size_t) b.n_items * 8);
-            HCK(hipMemcpy(ts.data(), reinterpret_cast<unsigned long long *>(b.part) + (size_t) b.n_items * b.R * HD / 2, ts.size() * 8,
-                          hipMemcpyDeviceToHost));
-            FILE * f = fopen(getenv("QKV_TIMING_FILE"), "ab");
-            if (f) {
-                fwrite(ts.data(), 8, ts.size(), f);
-                fclose(f);
-            }
-        }
-#endif
         for (const AttnArgs & b : groups) HCK(launch_combine(b, st));
         prof_mark(es, 2, st);
         return 0;

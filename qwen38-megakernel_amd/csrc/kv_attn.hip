@@ -1,16 +1,15 @@
-// Split-K decode attention over the mixed q8-ring / packed KV store (gfx950, wave64, MFMA f16), one kernel per call:
-// query preparation, the attention over every segment, and the merge of the segments into the output.
+// Split-K decode attention over the mixed q8-ring / packed KV store (gfx950, wave64, MFMA f16): k_attn computes the
+// query preparation and every segment's partial (m, l, O); k_combine merges a head's segments into the output.
 //
 // Work: one workgroup of 4 waves per (sequence, layer, kv head, canonical segment).  The segment length depends only on
 // L's 640-position bucket (seg_len), so the partition -- and with it every rounding -- is independent of the grid,
 // the split count and the number of query tokens sharing the bucket.  Wave w takes the 32-position tiles w, w+4, ..
-// of the segment with its own online-softmax state; the 4 states are merged in wave order into the segment's partial
-// (m, l, O); the last segment of each group of 8 to finish merges the group, and the last group merges the head
-// (fixed orders, so which workgroup performs a merge never changes a bit).
+// of the segment with its own online-softmax state; the 4 states are merged in wave order into the segment's partial.
+// k_combine merges the segments of a head in segment order (fixed orders: no bit depends on scheduling).
 //
-// Per tile and wave: the tile's packed rows are copied HBM -> LDS by global_load_lds_dwordx4 into one of two stages
-// (two tiles in flight per wave, 8 per CU), read into registers in MFMA operand layout, and the stage is refilled with
-// the tile after next before the math starts:
+// Per tile and wave: the tile's packed rows are copied HBM -> LDS by global_load_lds_dwordx4 into the wave's stage,
+// read into registers in MFMA operand layout, and the stage is refilled with the wave's next tile before the math
+// starts (one tile in flight per wave while it computes, 8 per CU at two workgroups per CU):
 //   S^T = K Q^T   v_mfma_f32_16x16x32_f16, A = 16 positions x 32 dims of K (lane: position l%16, 8 consecutive dims of
 //                 its quarter l/16 of the row), B = Q^T (lane: query row l%16, the same dims).  Two 16-position subtiles.
 //   softmax       lane (row l%16, quarter q) owns S of positions 4q..4q+3 and 16+4q..16+4q+3 of its row: 8 values,
@@ -322,9 +321,8 @@ __device__ __forceinline__ int qchunk(int r, int c) { return r * (HD / 8) + (c ^
 // the query fragment of row group rg, K step ks for lane (n, q): 8 fp16 dims 64 q + 8 ks .. of row 16 rg + n
 __device__ __forceinline__ half8 qfrag(const half8 * sQ, int rg, int ks, int n, int q) { return sQ[qchunk(16 * rg + n, 8 * q + ks)]; }
 
-// mid(raw) runs between the softmax and P V: it reads the V operands and releases the stage
-template <int NR, int KB, int VB, class Mid>
-__device__ __forceinline__ void compute_tile(WaveState<NR> & st, const half8 * sQ, int p0, RawTile<KB, VB> & raw, Mid mid) {
+template <int NR, int KB, int VB>
+__device__ __forceinline__ void compute_tile(WaveState<NR> & st, const half8 * sQ, int p0, const RawTile<KB, VB> & raw) {
     const int lane = lane_id(), q = lane >> 4, n = lane & 15;
     // ---- S^T = K Q^T
     f32x4 s[2][NR];
@@ -393,7 +391,6 @@ __device__ __forceinline__ void compute_tile(WaveState<NR> & st, const half8 * s
 #pragma unroll
             for (int i = 0; i < 16; i++) st.acc[rg][i] *= alpha[rg];
     }
-    mid(raw);
     // ---- O^T += V^T P^T, one instruction per dim 16 m + i of the lane
     half2v dv[4];
 #pragma unroll
@@ -436,10 +433,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NR == 1 ? 2
     const unsigned st_lds = (unsigned) __builtin_amdgcn_readfirstlane(lds0 + wv * STAGE_BYTES);
     half8 * const sQ = reinterpret_cast<half8 *>(smem + ATTN_LDS); // [RP][256] fp16, chunk-swizzled (qchunk)
     for (int item = blockIdx.x; item < a.n_items; item += gridDim.x) {
-#ifdef QKV_EXPERIMENT_TIMING
-        unsigned long long * tstamp = reinterpret_cast<unsigned long long *>(a.part) + (size_t) a.n_items * a.R * HD / 2 + (size_t) item * 8;
-        if (threadIdx.x == 0) tstamp[0] = __builtin_amdgcn_s_memrealtime();
-#endif
         int si = 0;
 #pragma unroll
         for (int i = 1; i < 8; i++)
@@ -511,9 +504,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NR == 1 ? 2
         __syncthreads(); // the query rows are complete
         const uint8_t * const stp = smem + wv * STAGE_BYTES; // (derived from smem: LDS reads)
         for (int i = 0; i < my; i++) {
-#ifndef QKV_EXPERIMENT_NOWAIT
             vm_wait<0>(); // tile i has landed (the wave's only copies in flight)
-#endif
             const int p0 = c0 + ATP * (wv + AWAVES * i);
             const bool ring = S.kvrc > 0 && p0 >= ws;
             // K operands now; V operands after the scores, then the stage is free and the next tile streams in during
@@ -524,29 +515,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NR == 1 ? 2
                 read_v<8, 8>(raw, stp, n, q);
                 lds_drain();
                 if (i + 1 < my) issue(i + 1);
-#ifndef QKV_EXPERIMENT_NOCOMPUTE
-                compute_tile<NR, 8, 8>(st, sQ, p0, raw, [](RawTile<8, 8> &) {});
-#else
-                st.acc[0][0][0] += __builtin_bit_cast(float, raw.k0.d[0] ^ raw.v.d[7][1]);
-#endif
+                compute_tile<NR, 8, 8>(st, sQ, p0, raw);
             } else {
                 RawTile<KB, VB> raw;
                 read_k<KB, VB>(raw, stp, n, q);
                 read_v<KB, VB>(raw, stp, n, q);
                 lds_drain();
                 if (i + 1 < my) issue(i + 1);
-#ifndef QKV_EXPERIMENT_NOCOMPUTE
-                compute_tile<NR, KB, VB>(st, sQ, p0, raw, [](RawTile<KB, VB> &) {});
-#else
-                st.acc[0][0][0] += __builtin_bit_cast(float, raw.k0.d[0] ^ raw.v.d[7][1]);
-#endif
+                compute_tile<NR, KB, VB>(st, sQ, p0, raw);
             }
         }
         // ---- merge the 4 waves in order: M = max m_w, O = sum e_w O_w, l = sum e_w l_w.  Every wave writes its
         // scaled O rows to its own LDS buffer (the stages are free), then each thread adds the 4 buffers in wave order.
-#ifdef QKV_EXPERIMENT_TIMING
-        if (lane == 0) tstamp[1 + wv] = __builtin_amdgcn_s_memrealtime();
-#endif
         constexpr int OLD = HD + 4;                                 // row stride (floats) of a wave's O buffer
         float * const s_m = reinterpret_cast<float *>(smem + AWAVES * 16 * OLD * 4); // [AWAVES][RP]
         float * const s_l = s_m + AWAVES * RP;                                        // [AWAVES][RP]
@@ -604,9 +584,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NR == 1 ? 2
             }
             a.ml[(size_t) item * R + row] = make_float2(M, lsum);
         }
-#ifdef QKV_EXPERIMENT_TIMING
-        if (threadIdx.x == 0) { tstamp[5] = __builtin_amdgcn_s_memrealtime(); tstamp[6] = __smid(); tstamp[7] = ntiles; }
-#endif
         __syncthreads(); // the LDS is reused by the next item
     }
 }

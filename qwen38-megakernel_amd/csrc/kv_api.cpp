@@ -407,7 +407,7 @@ int mk_kv_attend(void * h, int layer0, int n_layers, int n_seq, const int * seqs
         a.S = s.S;
         a.T = T;
         a.R = GQA * T;
-        a.RP = (a.R + 15) / 16 * 16;
+        a.RP = a.R <= 8 ? 8 : a.R <= 16 ? 16 : a.R <= 24 ? 24 : 48; // 8-row groups: 1, 2, 3 or 6 per kernel
         a.nseq = n_seq;
         int seg_total = 0;
         for (int i = 0; i < n_seq; i++) {

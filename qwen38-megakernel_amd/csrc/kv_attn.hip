@@ -11,11 +11,12 @@
 // read into registers in MFMA operand layout, and the stage is refilled with the wave's next tile before the math
 // starts (one tile in flight per wave while it computes, 8 per CU at two workgroups per CU):
 //   S^T = K Q^T   v_mfma_f32_16x16x32_f16, A = 16 positions x 32 dims of K (lane: position l%16, 8 consecutive dims of
-//                 its quarter l/16 of the row), B = Q^T (lane: query row l%16, the same dims).  Two 16-position subtiles.
-//   softmax       lane (row l%16, quarter q) owns S of positions 4q..4q+3 and 16+4q..16+4q+3 of its row: 8 values,
+//                 its quarter l/16 of the row), B = Q^T with column n = query row n/2 of an 8-row group (the tile
+//                 section below).  Two 16-position subtiles.
+//   softmax       lane (n, quarter q) owns the scores of its row at positions 4q..4q+3 and 16+4q..16+4q+3: 8 values,
 //                 max / sum across the 4 quarters by two xor shuffles; exp2 in log2 units.
-//   O^T += V^T P^T  A = V^T (lane: dims 16 (l%16) + i for instruction i, its 8 positions), B = P^T (the lane's own 8 P
-//                 values as fp16), C = O^T (lane: its row, dims 64q .. 64q+63).
+//   O += P V      the MFMA's K as 16 positions x 2 adjacent dims: A = two adjacent dims of one position of V,
+//                 B = P in the (row, dim parity) column pairs.
 // Dequantization happens in registers with the 0x6400 magic (kv_dev.h): fp16 values half_rn(d q), the reference's
 // operands (q8_to_f16 qwen38_mk.cu:2336, qn_to_f16 :2458).  The arithmetic of a row follows attn_core_t
 // (qwen38_mk.cu:2757-3080): S in fp32 from fp16 operands, masked positions -> -inf, P rounded to fp16, O in fp32.
@@ -306,124 +307,154 @@ __device__ __forceinline__ void read_v(RawTile<KB, VB> & r, const uint8_t * st, 
 }
 
 // ------------------------------------------------------------------------------------------------ the tile
-template <int NR>
+// Query rows go in NP groups of 8 (NP = ceil(6 T / 8), rounded up to 1, 2, 3 or 6).  Both MFMA products use the 16
+// columns as (row, e) pairs, row = 8 h + n / 2 of group h and e = n % 2:
+//   S^T = K Q^T   column n of Q^T is query row 8 h + n / 2 (each score is computed in lanes n and n ^ 1), so lane
+//                 (n, q) owns its row's scores at positions 4 q + e and 16 + 4 q + e (e = 0..3);
+//   O += P V      the MFMA's K = 32 is 16 positions x (e = 0, 1):
+//                 O[row][16 m + 2 b + e'] = sum_{p, e} A[m][(p, e)] B[(p, e)][(row, e')],
+//                 A = V[p][16 m + 2 b + e],  B = P[p][row] if e = e' else 0,
+//                 so an A register holds two adjacent dims of one position: a byte pair of the position's code word
+//                 and one scale per register, shared by every row group.
+// A row's arithmetic does not depend on its group or on T, so the partials are bitwise T-invariant.
+template <int NP>
 struct WaveState {
-    f32x4 acc[NR][16]; // O^T: instruction i, element e -> dim 64 q + 16 e + i of the lane's row
-    float m[NR], l[NR];
-    int lim[NR];       // last visible position of the lane's row (-1: padding row)
-    int lim_min;       // last position visible to every real row (L - T), wave-uniform
+    f32x4 acc[NP][8]; // group h, block b, element i -> dim 16 (4 q + i) + 2 b + (n & 1) of row 8 h + n / 2
+    float m[NP], l[NP];
+    int lim[NP];      // last visible position of the lane's row (-1: padding row)
+    int lim_min;      // last position visible to every real row (L - T), wave-uniform
 };
 
-// query rows in LDS: fp16 [RP][256] with 16-byte chunk c of row r stored at chunk c ^ (r % 16), so the 16 rows one
-// fragment read touches hit 16 different bank groups
+// query rows in LDS: fp16 [RP][256] with 16-byte chunk c of row r stored at chunk c ^ (r % 16)
 __device__ __forceinline__ int qchunk(int r, int c) { return r * (HD / 8) + (c ^ (r & 15)); }
 
-// the query fragment of row group rg, K step ks for lane (n, q): 8 fp16 dims 64 q + 8 ks .. of row 16 rg + n
-__device__ __forceinline__ half8 qfrag(const half8 * sQ, int rg, int ks, int n, int q) { return sQ[qchunk(16 * rg + n, 8 * q + ks)]; }
-
-template <int NR, int KB, int VB>
-__device__ __forceinline__ void compute_tile(WaveState<NR> & st, const half8 * sQ, int p0, const RawTile<KB, VB> & raw) {
+template <int NP, int KB, int VB>
+__device__ __forceinline__ void compute_tile(WaveState<NP> & st, const half8 * sQ, int p0, const RawTile<KB, VB> & raw) {
     const int lane = lane_id(), q = lane >> 4, n = lane & 15;
-    // ---- S^T = K Q^T
-    f32x4 s[2][NR];
+    // ---- S^T = K Q^T, two 16-position subtiles
+    f32x4 s[NP][2];
 #pragma unroll
-    for (int rg = 0; rg < NR; rg++) s[0][rg] = s[1][rg] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int h = 0; h < NP; h++) s[h][0] = s[h][1] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int ks = 0; ks < 8; ks++) {
         const half8 a0 = kfrag<KB>(raw.k0, ks);
         const half8 a1 = kfrag<KB>(raw.k1, ks);
 #pragma unroll
-        for (int rg = 0; rg < NR; rg++) {
-            const half8 b = qfrag(sQ, rg, ks, n, q);
-            s[0][rg] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, b, s[0][rg], 0, 0, 0);
-            s[1][rg] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, b, s[1][rg], 0, 0, 0);
+        for (int h = 0; h < NP; h++) {
+            const half8 b = sQ[qchunk(8 * h + (n >> 1), 8 * q + ks)];
+            s[h][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, b, s[h][0], 0, 0, 0);
+            s[h][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, b, s[h][1], 0, 0, 0);
         }
     }
-    // ---- online softmax (log2 units); lane: its row, positions p0 + 4q + e and p0 + 16 + 4q + e.
-    // The running max moves only when a tile's max exceeds it by more than RESCALE_LOG2 (and on the first visible
-    // tile): until then P = exp2(s - m) <= 2^RESCALE_LOG2 (exact in fp16 range) and O, l keep their scale, so most
-    // tiles need no rescale of O.  A function of the data order within the fixed partition only: deterministic.
+    // ---- online softmax (log2 units).  The running max moves only when a tile's max exceeds it by more than
+    // RESCALE_LOG2 (and on the first visible tile): until then P = exp2(s - m) <= 2^RESCALE_LOG2 (in fp16 range) and
+    // O, l keep their scale, so most tiles need no rescale of O.  A function of the data order within the fixed
+    // partition only: deterministic.
     constexpr float RESCALE_LOG2 = 8.f;
-    half8 pf[NR];
+    const bool full = p0 + ATP - 1 <= st.lim_min; // every position of the tile visible to every row (uniform)
+    float p[NP][8], alpha[NP];
     bool rescale = false;
-    float alpha[NR];
 #pragma unroll
-    for (int rg = 0; rg < NR; rg++) {
+    for (int h = 0; h < NP; h++) {
         float t[8];
         float mx = -INFINITY;
-        const bool full = p0 + ATP - 1 <= st.lim_min; // every position of the tile visible to every row (uniform)
 #pragma unroll
         for (int e = 0; e < 8; e++) {
             const int pos = p0 + (e < 4 ? 4 * q + e : 16 + 4 * q + e - 4);
-            const float sv = (e < 4 ? s[0][rg][e] : s[1][rg][e - 4]) * LOG2E;
-            t[e] = full || pos <= st.lim[rg] ? sv : -INFINITY;
+            const float sv = (e < 4 ? s[h][0][e] : s[h][1][e - 4]) * LOG2E;
+            t[e] = full || pos <= st.lim[h] ? sv : -INFINITY;
             mx = fmaxf(mx, t[e]);
         }
         mx = fmaxf(mx, shfl_xor(mx, 16));
         mx = fmaxf(mx, shfl_xor(mx, 32));
-        const float mold = st.m[rg];
+        const float mold = st.m[h];
         const float mnew = mx > mold + RESCALE_LOG2 ? mx : mold; // (mold = -inf: any finite mx)
         float al = 1.f, ps = 0.f;
-        float p[8];
         if (mnew != -INFINITY) {
             al = mold == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mold - mnew);
 #pragma unroll
             for (int e = 0; e < 8; e++) {
-                p[e] = __builtin_amdgcn_exp2f(t[e] - mnew);
-                ps += p[e];
+                p[h][e] = __builtin_amdgcn_exp2f(t[e] - mnew);
+                ps += p[h][e];
             }
         } else {
 #pragma unroll
-            for (int e = 0; e < 8; e++) p[e] = 0.f;
+            for (int e = 0; e < 8; e++) p[h][e] = 0.f;
         }
         ps += shfl_xor(ps, 16);
         ps += shfl_xor(ps, 32);
-        st.l[rg] = __builtin_fmaf(st.l[rg], al, ps);
-        st.m[rg] = mnew;
-        alpha[rg] = al;
+        st.l[h] = __builtin_fmaf(st.l[h], al, ps);
+        st.m[h] = mnew;
+        alpha[h] = al;
         rescale |= al != 1.f && mold != -INFINITY; // (O is still zero before the first visible tile)
-#pragma unroll
-        for (int e = 0; e < 8; e++) pf[rg][e] = (_Float16) p[e];
     }
     if (__any(rescale)) { // alpha == 1 exactly leaves O unchanged: the skip is exact
 #pragma unroll
-        for (int rg = 0; rg < NR; rg++)
+        for (int h = 0; h < NP; h++)
 #pragma unroll
-            for (int i = 0; i < 16; i++) st.acc[rg][i] *= alpha[rg];
+            for (int b = 0; b < 8; b++) st.acc[h][b] *= alpha[h];
     }
-    // ---- O^T += V^T P^T, one instruction per dim 16 m + i of the lane
-    half2v dv[4];
+    // ---- B operands of the two 16-position groups G: (P, 0) in even columns, (0, P) in odd ones
+    const unsigned odd = n & 1;
+    const unsigned sel_lo = odd ? 0x05040c0cu : 0x0c0c0504u, sel_hi = odd ? 0x07060c0cu : 0x0c0c0706u;
+    half8 pb[NP][2];
 #pragma unroll
-    for (int jp = 0; jp < 4; jp++) dv[jp] = as_h2((raw.v.s[2 * jp] & 0xffffu) | (raw.v.s[2 * jp + 1] << 16));
-    constexpr unsigned XMAG = VB == 8 ? 0x64806480u : 0x64006400u;
+    for (int h = 0; h < NP; h++)
+#pragma unroll
+        for (int G = 0; G < 2; G++)
+#pragma unroll
+            for (int k = 0; k < 2; k++) {
+                half2v x2;
+                x2[0] = (_Float16) p[h][4 * G + 2 * k];
+                x2[1] = (_Float16) p[h][4 * G + 2 * k + 1];
+                const unsigned x = as_u(x2);
+                const half2v y0 = as_h2(perm_b32(x, 0u, sel_lo)), y1 = as_h2(perm_b32(x, 0u, sel_hi));
+                pb[h][G][4 * k] = y0[0];
+                pb[h][G][4 * k + 1] = y0[1];
+                pb[h][G][4 * k + 2] = y1[0];
+                pb[h][G][4 * k + 3] = y1[1];
+            }
+    // ---- O += P V: block b = dims 16 m + 2 b, + 1 of the lane's V row m (nibble word b / 4, values 2 (b % 4), + 1)
+    half2v dv[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) dv[j] = as_h2((raw.v.s[j] & 0xffffu) * 0x10001u);
+    constexpr unsigned QX = VB == 8 ? 0x80808080u : 0u; // q8: signed byte -> byte + 128
     constexpr float VBIAS = VB == 8 ? 1152.f : (float) (1024 + (1 << (VB - 1)));
     const half2v vb2 = {(_Float16) -VBIAS, (_Float16) -VBIAS};
 #pragma unroll
-    for (int w = 0; w < 2; w++) { // nibble word w of the lane: dims 16 m + 8 w .. + 7 (two code registers per position)
+    for (int w = 0; w < 2; w++) {
         unsigned c[8][2];
 #pragma unroll
-        for (int j = 0; j < 8; j++) vcodes_word<VB>(raw.v, j, w, c[j]);
+        for (int j = 0; j < 8; j++) {
+            vcodes_word<VB>(raw.v, j, w, c[j]);
+            c[j][0] ^= QX;
+            c[j][1] ^= QX;
+        }
 #pragma unroll
-        for (int i8 = 0; i8 < 8; i8++) {
-            const int i = 8 * w + i8, a2 = i8 >> 2, b = i8 & 3;
-            const unsigned sel = (unsigned) b | 0x0c00u | ((unsigned) (4 + b) << 16) | 0x0c000000u;
-            half8 va;
+        for (int bb = 0; bb < 4; bb++) {
+            const int b = 4 * w + bb;
+            const unsigned sel = (bb & 1) ? 0x00070006u : 0x00050004u;
 #pragma unroll
-            for (int jp = 0; jp < 4; jp++) {
-                const half2v x = (as_h2(perm_b32(c[2 * jp + 1][a2], c[2 * jp][a2], sel) ^ XMAG) + vb2) * dv[jp];
-                va[2 * jp] = x[0];
-                va[2 * jp + 1] = x[1];
+            for (int G = 0; G < 2; G++) {
+                half8 va;
+#pragma unroll
+                for (int jj = 0; jj < 4; jj++) {
+                    const int j = 4 * G + jj;
+                    const half2v x = (as_h2(perm_b32(c[j][bb >> 1], C64, sel)) + vb2) * dv[j];
+                    va[2 * jj] = x[0];
+                    va[2 * jj + 1] = x[1];
+                }
+#pragma unroll
+                for (int h = 0; h < NP; h++) st.acc[h][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb[h][G], st.acc[h][b], 0, 0, 0);
             }
-#pragma unroll
-            for (int rg = 0; rg < NR; rg++) st.acc[rg][i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pf[rg], st.acc[rg][i], 0, 0, 0);
         }
     }
 }
 
 // ------------------------------------------------------------------------------------------------ the kernel
-template <int NR, int KB, int VB>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NR == 1 ? 2 : 1, NR == 1 ? 2 : 1))) void k_attn(AttnArgs a) {
-    constexpr int RP = 16 * NR;
+template <int NP, int KB, int VB>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NP == 1 ? 2 : 1, NP == 1 ? 2 : 1))) void k_attn(AttnArgs a) {
+    constexpr int RP = 8 * NP; // query rows held (the padding rows are zero)
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     // the wave index as a scalar: tile positions, page lookups and source selection stay scalar (SMEM loads, uniform
     // branches); vector loads there would need vmcnt waits that also drain the tile copies in flight
@@ -490,15 +521,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NR == 1 ? 2
             }
             reinterpret_cast<uint2 *>(sQ + qchunk(r, lane >> 1))[lane & 1] = make_uint2(as_u(o0), as_u(o1));
         }
-        WaveState<NR> st;
+        WaveState<NP> st;
 #pragma unroll
-        for (int rg = 0; rg < NR; rg++) {
-            st.m[rg] = -INFINITY;
-            st.l[rg] = 0.f;
-            const int row = 16 * rg + n;
-            st.lim[rg] = row < a.R ? L - T + row % T : -1;
+        for (int h = 0; h < NP; h++) {
+            st.m[h] = -INFINITY;
+            st.l[h] = 0.f;
+            const int row = 8 * h + (n >> 1);
+            st.lim[h] = row < a.R ? L - T + row % T : -1;
 #pragma unroll
-            for (int i = 0; i < 16; i++) st.acc[rg][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+            for (int b = 0; b < 8; b++) st.acc[h][b] = f32x4{0.f, 0.f, 0.f, 0.f};
         }
         st.lim_min = L - T;
         __syncthreads(); // the query rows are complete
@@ -507,56 +538,59 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NR == 1 ? 2
             vm_wait<0>(); // tile i has landed (the wave's only copies in flight)
             const int p0 = c0 + ATP * (wv + AWAVES * i);
             const bool ring = S.kvrc > 0 && p0 >= ws;
-            // K operands now; V operands after the scores, then the stage is free and the next tile streams in during
-            // this one's P V
+            // operands into registers, then the stage is free and the next tile streams in during this one's math
             if (ring) {
                 RawTile<8, 8> raw;
                 read_k<8, 8>(raw, stp, n, q);
                 read_v<8, 8>(raw, stp, n, q);
                 lds_drain();
                 if (i + 1 < my) issue(i + 1);
-                compute_tile<NR, 8, 8>(st, sQ, p0, raw);
+                compute_tile<NP, 8, 8>(st, sQ, p0, raw);
             } else {
                 RawTile<KB, VB> raw;
                 read_k<KB, VB>(raw, stp, n, q);
                 read_v<KB, VB>(raw, stp, n, q);
                 lds_drain();
                 if (i + 1 < my) issue(i + 1);
-                compute_tile<NR, KB, VB>(st, sQ, p0, raw);
+                compute_tile<NP, KB, VB>(st, sQ, p0, raw);
             }
         }
-        // ---- merge the 4 waves in order: M = max m_w, O = sum e_w O_w, l = sum e_w l_w.  Every wave writes its
-        // scaled O rows to its own LDS buffer (the stages are free), then each thread adds the 4 buffers in wave order.
-        constexpr int OLD = HD + 4;                                 // row stride (floats) of a wave's O buffer
+        // ---- merge the 4 waves in order: M = max m_w, O = sum e_w O_w, l = sum e_w l_w.  Per pass of 16 rows (two
+        // groups) every wave writes its scaled O rows to its own LDS buffer (the stages are free), then each thread
+        // adds the 4 buffers in wave order.
+        constexpr int OLD = HD + 4;                                                   // row stride (floats) of a buffer
         float * const s_m = reinterpret_cast<float *>(smem + AWAVES * 16 * OLD * 4); // [AWAVES][RP]
         float * const s_l = s_m + AWAVES * RP;                                        // [AWAVES][RP]
-        static_assert(AWAVES * 16 * OLD * 4 + 2 * AWAVES * 3 * 16 * 4 <= ATTN_LDS, "merge buffers inside the stages");
+        static_assert(AWAVES * 16 * OLD * 4 + 2 * AWAVES * 48 * 4 <= ATTN_LDS, "merge buffers inside the stages");
         __syncthreads(); // every wave is done with its stage
-        if (q == 0) {
+        if (q == 0 && !(n & 1)) {
 #pragma unroll
-            for (int rg = 0; rg < NR; rg++) {
-                s_m[wv * RP + 16 * rg + n] = st.m[rg];
-                s_l[wv * RP + 16 * rg + n] = st.l[rg];
+            for (int h = 0; h < NP; h++) {
+                s_m[wv * RP + 8 * h + (n >> 1)] = st.m[h];
+                s_l[wv * RP + 8 * h + (n >> 1)] = st.l[h];
             }
         }
         __syncthreads();
         const int R = a.R;
+        constexpr int NPASS = (NP + 1) / 2;
 #pragma unroll
-        for (int rg = 0; rg < NR; rg++) { // one 16-row group per pass: every wave writes, then all threads add
-            {
-                const int row = 16 * rg + n;
-                const float M = fmaxf(fmaxf(s_m[row], s_m[RP + row]), fmaxf(s_m[2 * RP + row], s_m[3 * RP + row]));
-                const float e = st.m[rg] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(st.m[rg] - M);
-                float * o = reinterpret_cast<float *>(smem) + (wv * 16 + n) * OLD + 64 * q;
+        for (int ps = 0; ps < NPASS; ps++) {
 #pragma unroll
-                for (int ee = 0; ee < 4; ee++)
+            for (int hh = 0; hh < 2; hh++) {
+                const int h = 2 * ps + hh;
+                if (h < NP) {
+                    const int row = 8 * h + (n >> 1);
+                    const float M = fmaxf(fmaxf(s_m[row], s_m[RP + row]), fmaxf(s_m[2 * RP + row], s_m[3 * RP + row]));
+                    const float e = st.m[h] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(st.m[h] - M);
+                    float * o = reinterpret_cast<float *>(smem) + (wv * 16 + 8 * hh + (n >> 1)) * OLD + 64 * q + (n & 1);
 #pragma unroll
-                    for (int i4 = 0; i4 < 16; i4 += 4) // dims 64 q + 16 ee + i4 .. + 3
-                        *reinterpret_cast<float4 *>(o + 16 * ee + i4) =
-                            make_float4(e * st.acc[rg][i4][ee], e * st.acc[rg][i4 + 1][ee], e * st.acc[rg][i4 + 2][ee], e * st.acc[rg][i4 + 3][ee]);
+                    for (int b = 0; b < 8; b++)
+#pragma unroll
+                        for (int i = 0; i < 4; i++) o[16 * i + 2 * b] = e * st.acc[h][b][i];
+                }
             }
             __syncthreads();
-            const int nrow = min(16, R - 16 * rg);
+            const int nrow = min(16, R - 16 * ps);
             for (int idx = threadIdx.x; idx < nrow * (HD / 4); idx += 256) {
                 const int r16 = idx / (HD / 4), c4 = idx % (HD / 4);
                 const float * src = reinterpret_cast<const float *>(smem) + r16 * OLD + 4 * c4;
@@ -569,9 +603,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NR == 1 ? 2
                     y.z += z.z;
                     y.w += z.w;
                 }
-                *reinterpret_cast<float4 *>(a.part + ((size_t) item * R + 16 * rg + r16) * HD + 4 * c4) = y;
+                *reinterpret_cast<float4 *>(a.part + ((size_t) item * R + 16 * ps + r16) * HD + 4 * c4) = y;
             }
-            if (rg + 1 < NR) __syncthreads();
+            if (ps + 1 < NPASS) __syncthreads();
         }
         if (threadIdx.x < R) {
             const int row = threadIdx.x;
@@ -589,13 +623,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NR == 1 ? 2
 }
 
 // ------------------------------------------------------------------------------------------------ combine
-// One workgroup per output row (layer, sequence, kv head, row r): the canonical merge of the head's segment partials
-// (attn_combine, qwen38_mk.cu:4617-4700): M = max m (exact, order-free), e_c = exp2(m_c - M) (0 for m = -inf);
-// wave w sums the segments c = w, w+4, .. in order (all its loads issued together), the four sums are added in wave
-// order; y = O / l, then the V un-rotation when V is stored rotated.  The order is fixed by the segment index alone.
+// One workgroup per output row (layer, sequence, kv head, row r): the merge of the head's segment partials
+// (attn_combine, qwen38_mk.cu:4617-4700: y = sum_c e_c O_c / sum_c e_c l_c with e_c = exp(m_c - M)).  Wave w loads the
+// segments c = w, w+4, .. at once, weights them by exp2(m_c - M_w) against its own maximum M_w and sums them in
+// segment order; the four wave sums are rescaled to M = max M_w and added in wave order; y = O / l, then the V
+// un-rotation when V is stored rotated.  The order is fixed by the segment index alone.
 __global__ __launch_bounds__(256) void k_combine(AttnArgs a) {
     __shared__ float4 s_num[AWAVES][64];
-    __shared__ float s_den[AWAVES];
+    __shared__ float2 s_md[AWAVES]; // (max, denominator) of each wave's segments
     const int R = a.R, T = a.T;
     int b = blockIdx.x;
     const int r = b % R;
@@ -607,10 +642,7 @@ __global__ __launch_bounds__(256) void k_combine(AttnArgs a) {
     const int nseg = sd.nseg;
     const size_t head0 = (size_t) sd.item0 + (size_t) (l * NKV + g) * nseg;
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-    float M = -INFINITY;
-    for (int c = lane; c < nseg; c += 64) M = fmaxf(M, a.ml[(head0 + c) * R + r].x);
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) M = fmaxf(M, shfl_xor(M, o));
+    // one round of loads: wave w's segments c = w, w + 4, .. (all issued before any is used)
     constexpr int PER = MAX_SEG / AWAVES;
     float2 ml[PER];
     float4 o[PER];
@@ -622,13 +654,17 @@ __global__ __launch_bounds__(256) void k_combine(AttnArgs a) {
             o[k] = *reinterpret_cast<const float4 *>(a.part + ((head0 + c) * R + r) * HD + 4 * lane);
         }
     }
+    float Mw = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < PER; k++)
+        if (wv + AWAVES * k < nseg) Mw = fmaxf(Mw, ml[k].x);
     float4 num = make_float4(0.f, 0.f, 0.f, 0.f);
     float den = 0.f;
 #pragma unroll
     for (int k = 0; k < PER; k++) {
         const int c = wv + AWAVES * k;
         if (c < nseg) {
-            const float e = ml[k].x == -INFINITY ? 0.f : exp2f(ml[k].x - M);
+            const float e = ml[k].x == -INFINITY ? 0.f : exp2f(ml[k].x - Mw);
             num.x = __builtin_fmaf(e, o[k].x, num.x);
             num.y = __builtin_fmaf(e, o[k].y, num.y);
             num.z = __builtin_fmaf(e, o[k].z, num.z);
@@ -637,19 +673,25 @@ __global__ __launch_bounds__(256) void k_combine(AttnArgs a) {
         }
     }
     s_num[wv][lane] = num;
-    if (lane == 0) s_den[wv] = den;
+    if (lane == 0) s_md[wv] = make_float2(Mw, den);
     __syncthreads();
     if (wv != 0) return;
-    float4 y = s_num[0][lane];
-    float dd = s_den[0];
+    // the 4 wave sums in wave order, each rescaled to the overall max
+    float M = s_md[0].x;
 #pragma unroll
-    for (int k = 1; k < AWAVES; k++) {
+    for (int k = 1; k < AWAVES; k++) M = fmaxf(M, s_md[k].x);
+    float4 y = make_float4(0.f, 0.f, 0.f, 0.f);
+    float dd = 0.f;
+#pragma unroll
+    for (int k = 0; k < AWAVES; k++) {
+        const float2 md = s_md[k];
+        const float e = md.x == -INFINITY ? 0.f : exp2f(md.x - M);
         const float4 z = s_num[k][lane];
-        y.x += z.x;
-        y.y += z.y;
-        y.z += z.z;
-        y.w += z.w;
-        dd += s_den[k];
+        y.x = __builtin_fmaf(e, z.x, y.x);
+        y.y = __builtin_fmaf(e, z.y, y.y);
+        y.z = __builtin_fmaf(e, z.z, y.z);
+        y.w = __builtin_fmaf(e, z.w, y.w);
+        dd = __builtin_fmaf(e, md.y, dd);
     }
     float v[4] = {y.x / dd, y.y / dd, y.z / dd, y.w / dd};
     if ((a.vrot >> (a.layer0 + l)) & 1u) fwht256_w64(v);
@@ -665,15 +707,15 @@ hipError_t launch_combine(const AttnArgs & a, hipStream_t st) {
 // ------------------------------------------------------------------------------------------------ dispatch
 typedef void (*AttnKernel)(AttnArgs);
 
-template <int NR>
+template <int NP>
 static AttnKernel pick(int kb, int vb) {
 #define QKV_VB(K)                                                                                                      \
     switch (vb) {                                                                                                      \
-    case 4: return k_attn<NR, K, 4>;                                                                                   \
-    case 5: return k_attn<NR, K, 5>;                                                                                   \
-    case 6: return k_attn<NR, K, 6>;                                                                                   \
-    case 7: return k_attn<NR, K, 7>;                                                                                   \
-    case 8: return k_attn<NR, K, 8>;                                                                                   \
+    case 4: return k_attn<NP, K, 4>;                                                                                   \
+    case 5: return k_attn<NP, K, 5>;                                                                                   \
+    case 6: return k_attn<NP, K, 6>;                                                                                   \
+    case 7: return k_attn<NP, K, 7>;                                                                                   \
+    case 8: return k_attn<NP, K, 8>;                                                                                   \
     default: return nullptr;                                                                                           \
     }
     switch (kb) {
@@ -689,10 +731,11 @@ static AttnKernel pick(int kb, int vb) {
 
 hipError_t launch_attn(const AttnArgs & a, int kb, int vb, int max_blocks, hipStream_t st) {
     AttnKernel k = nullptr;
-    const int nr = a.RP / 16;
-    if (nr == 1) k = pick<1>(kb, vb);
-    else if (nr == 2) k = pick<2>(kb, vb);
-    else if (nr == 3) k = pick<3>(kb, vb);
+    const int np = a.RP / 8;
+    if (np == 1) k = pick<1>(kb, vb);
+    else if (np == 2) k = pick<2>(kb, vb);
+    else if (np == 3) k = pick<3>(kb, vb);
+    else if (np == 6) k = pick<6>(kb, vb);
     if (!k) return hipErrorInvalidValue;
     static thread_local const void * configured[128];
     static thread_local int n_configured = 0;

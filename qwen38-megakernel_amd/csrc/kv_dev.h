@@ -121,10 +121,12 @@ __device__ __forceinline__ unsigned as_u(half2v x) { return __builtin_bit_cast(u
 // the hb-bit fields 0..3 of x (field k at bit hb k) moved to bits 4 .. 4+hb-1 of byte k
 template <int HB>
 __device__ __forceinline__ unsigned spread4(unsigned x) {
-    if constexpr (HB == 1) return (((x & 0xfu) * 0x00204081u) & 0x01010101u) << 4; // bit k -> bit 8k (copies disjoint)
+    // 24-bit multiplies (full rate): the compiler cannot always prove the operands fit and would otherwise emit the
+    // quarter-rate 32-bit multiply
+    if constexpr (HB == 1) return __umul24((x << 4) & 0xf0u, 0x00204081u) & 0x10101010u; // bit k -> bit 8k + 4
     if constexpr (HB == 2) {
-        x = ((x & 0xffu) * 0x10010u) & 0x00f000f0u; // fields 0,1 at bits 4..7, fields 2,3 at 20..23
-        return (x * 0x41u) & 0x30303030u;          // field 1 -> 12..13, field 3 -> 28..29
+        x = __umul24(x & 0xffu, 0x10010u) & 0x00f000f0u; // fields 0,1 at bits 4..7, fields 2,3 at 20..23
+        return __umul24(x, 0x41u) & 0x30303030u;       // field 1 -> 12..13, field 3 -> 28..29
     }
     if constexpr (HB == 3) {
         x &= 0xfffu;

@@ -19,7 +19,7 @@ struct AttnArgs {
     StoreLayout S;
     int layer0;          // first slot of the launch
     int nl;              // layers in the launch (all with the same K/V bits)
-    int T, R, RP;        // query tokens, query rows per kv head (6 T), rows padded to 16 per MFMA row group
+    int T, R, RP;        // query tokens, query rows per kv head (6 T), rows held in 8-row groups (8, 16, 24 or 48)
     int nseq;
     int n_items;         // (sequence, layer, kv head, segment) work items
     unsigned krot, vrot; // per-slot bit masks: K / V stored rotated

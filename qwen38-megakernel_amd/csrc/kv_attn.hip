@@ -14,7 +14,7 @@
 //                 its quarter l/16 of the row), B = Q^T with column n = query row n/2 of an 8-row group (the tile
 //                 section below).  Two 16-position subtiles.
 //   softmax       lane (n, quarter q) owns the scores of its row at positions 4q..4q+3 and 16+4q..16+4q+3: 8 values,
-//                 max / sum across the 4 quarters by two xor shuffles; exp2 in log2 units.
+//                 max / sum across the 4 quarters by v_permlane16/32_swap; exp2 in log2 units.
 //   O += P V      the MFMA's K as 16 positions x 2 adjacent dims: A = two adjacent dims of one position of V,
 //                 B = P in the (row, dim parity) column pairs.
 // Dequantization happens in registers with the 0x6400 magic (kv_dev.h): fp16 values half_rn(d q), the reference's
@@ -365,8 +365,7 @@ __device__ __forceinline__ void compute_tile(WaveState<NP> & st, const half8 * s
             t[e] = full || pos <= st.lim[h] ? sv : -INFINITY;
             mx = fmaxf(mx, t[e]);
         }
-        mx = fmaxf(mx, shfl_xor(mx, 16));
-        mx = fmaxf(mx, shfl_xor(mx, 32));
+        mx = quad_max(mx);
         const float mold = st.m[h];
         const float mnew = mx > mold + RESCALE_LOG2 ? mx : mold; // (mold = -inf: any finite mx)
         float al = 1.f, ps = 0.f;
@@ -381,8 +380,7 @@ __device__ __forceinline__ void compute_tile(WaveState<NP> & st, const half8 * s
 #pragma unroll
             for (int e = 0; e < 8; e++) p[h][e] = 0.f;
         }
-        ps += shfl_xor(ps, 16);
-        ps += shfl_xor(ps, 32);
+        ps = quad_sum(ps);
         st.l[h] = __builtin_fmaf(st.l[h], al, ps);
         st.m[h] = mnew;
         alpha[h] = al;
@@ -449,6 +447,16 @@ __device__ __forceinline__ void compute_tile(WaveState<NP> & st, const half8 * s
             }
         }
     }
+}
+
+// wave issue priority 0..3 from the tiles a wave has left: the instruction arbiter otherwise favours the older
+// workgroup on a CU, which then finishes early and leaves the younger one's waves to run the launch's tail alone.
+// A uniform value; s_setprio takes an immediate.
+__device__ __forceinline__ void set_prio(int left) {
+    if (left >= 6) __builtin_amdgcn_s_setprio(3);
+    else if (left >= 5) __builtin_amdgcn_s_setprio(2);
+    else if (left >= 4) __builtin_amdgcn_s_setprio(1);
+    else __builtin_amdgcn_s_setprio(0);
 }
 
 // ------------------------------------------------------------------------------------------------ the kernel
@@ -535,6 +543,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NP == 1 ? 2
         __syncthreads(); // the query rows are complete
         const uint8_t * const stp = smem + wv * STAGE_BYTES; // (derived from smem: LDS reads)
         for (int i = 0; i < my; i++) {
+            set_prio(my - i);
             vm_wait<0>(); // tile i has landed (the wave's only copies in flight)
             const int p0 = c0 + ATP * (wv + AWAVES * i);
             const bool ring = S.kvrc > 0 && p0 >= ws;
@@ -699,8 +708,93 @@ __global__ __launch_bounds__(256) void k_combine(AttnArgs a) {
     *reinterpret_cast<float4 *>(a.out + (((size_t) (l * a.nseq + si) * T + t) * NH + h) * HD + 4 * lane) = make_float4(v[0], v[1], v[2], v[3]);
 }
 
+// The same merge for launches without rotated V, spread wider: one workgroup per (output row, 64-dim quarter).  Lane
+// group s = 4 w + l / 16 (16 per workgroup) takes the segments c = s, s + 16, .. (all loads at once), weights them by
+// exp2(m_c - M_s) against its own maximum and sums them in segment order; the 4 groups of a wave are merged by
+// permlane swaps, the 4 waves in wave order, each sum rescaled to the overall maximum; y = O / l.
+__global__ __launch_bounds__(256) void k_combine_split(AttnArgs a) {
+    __shared__ float4 s_num[AWAVES][16];
+    __shared__ float2 s_md[AWAVES];
+    const int R = a.R, T = a.T;
+    int b = blockIdx.x;
+    const int dq = b & 3;
+    b >>= 2;
+    const int r = b % R;
+    b /= R;
+    const int g = b % NKV;
+    b /= NKV;
+    const int si = b % a.nseq, l = b / a.nseq;
+    const SeqDesc & sd = a.sd[si];
+    const int nseg = sd.nseg;
+    const size_t head0 = (size_t) sd.item0 + (size_t) (l * NKV + g) * nseg;
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, sub = lane >> 4, dl = lane & 15;
+    const int slot = 4 * wv + sub, dim = 64 * dq + 4 * dl;
+    constexpr int PER = MAX_SEG / 16;
+    float2 ml[PER];
+    float4 o[PER];
+#pragma unroll
+    for (int k = 0; k < PER; k++) {
+        const int c = slot + 16 * k;
+        if (c < nseg) {
+            ml[k] = a.ml[(head0 + c) * R + r];
+            o[k] = *reinterpret_cast<const float4 *>(a.part + ((head0 + c) * R + r) * HD + dim);
+        }
+    }
+    float Ms = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < PER; k++)
+        if (slot + 16 * k < nseg) Ms = fmaxf(Ms, ml[k].x);
+    float4 num = make_float4(0.f, 0.f, 0.f, 0.f);
+    float den = 0.f;
+#pragma unroll
+    for (int k = 0; k < PER; k++) {
+        if (slot + 16 * k < nseg) {
+            const float e = ml[k].x == -INFINITY ? 0.f : exp2f(ml[k].x - Ms);
+            num.x = __builtin_fmaf(e, o[k].x, num.x);
+            num.y = __builtin_fmaf(e, o[k].y, num.y);
+            num.z = __builtin_fmaf(e, o[k].z, num.z);
+            num.w = __builtin_fmaf(e, o[k].w, num.w);
+            den = __builtin_fmaf(e, ml[k].y, den);
+        }
+    }
+    // the wave's 4 lane groups (same dims, slots 4 w .. 4 w + 3)
+    const float Mw = quad_max(Ms);
+    const float ew = Ms == -INFINITY ? 0.f : exp2f(Ms - Mw);
+    num.x = quad_sum(ew * num.x);
+    num.y = quad_sum(ew * num.y);
+    num.z = quad_sum(ew * num.z);
+    num.w = quad_sum(ew * num.w);
+    den = quad_sum(ew * den);
+    if (sub == 0) s_num[wv][dl] = num;
+    if (lane == 0) s_md[wv] = make_float2(Mw, den);
+    __syncthreads();
+    if (wv != 0 || sub != 0) return;
+    float M = s_md[0].x;
+#pragma unroll
+    for (int k = 1; k < AWAVES; k++) M = fmaxf(M, s_md[k].x);
+    float4 y = make_float4(0.f, 0.f, 0.f, 0.f);
+    float dd = 0.f;
+#pragma unroll
+    for (int k = 0; k < AWAVES; k++) {
+        const float2 md = s_md[k];
+        const float e = md.x == -INFINITY ? 0.f : exp2f(md.x - M);
+        const float4 z = s_num[k][dl];
+        y.x = __builtin_fmaf(e, z.x, y.x);
+        y.y = __builtin_fmaf(e, z.y, y.y);
+        y.z = __builtin_fmaf(e, z.z, y.z);
+        y.w = __builtin_fmaf(e, z.w, y.w);
+        dd = __builtin_fmaf(e, md.y, dd);
+    }
+    const int h = GQA * g + r / T, t = r % T;
+    *reinterpret_cast<float4 *>(a.out + (((size_t) (l * a.nseq + si) * T + t) * NH + h) * HD + dim) =
+        make_float4(y.x / dd, y.y / dd, y.z / dd, y.w / dd);
+}
+
 hipError_t launch_combine(const AttnArgs & a, hipStream_t st) {
-    hipLaunchKernelGGL(k_combine, dim3(a.nl * a.nseq * NKV * a.R), dim3(256), 0, st, a);
+    const unsigned rows = (unsigned) (a.nl * a.nseq * NKV * a.R);
+    const unsigned vrot = (a.vrot >> a.layer0) & ((a.nl >= 32 ? 0u : 1u << a.nl) - 1u);
+    if (vrot) hipLaunchKernelGGL(k_combine, dim3(rows), dim3(256), 0, st, a);
+    else hipLaunchKernelGGL(k_combine_split, dim3(4 * rows), dim3(256), 0, st, a);
     return hipGetLastError();
 }
 

@@ -23,6 +23,27 @@ __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
 __device__ __forceinline__ float shfl_xor(float v, int m) { return __shfl_xor(v, m, 64); }
 __device__ __forceinline__ unsigned shfl_xor_u(unsigned v, int m) { return (unsigned) __shfl_xor((int) v, m, 64); }
 
+// max / sum over the four lanes l, l ^ 16, l ^ 32, l ^ 48 with v_permlane16_swap / v_permlane32_swap (VALU exchanges
+// between 16-lane rows, no LDS round trip).  Two copies of the value go in; afterwards one register holds rows
+// (0, 0, 2, 2) and the other rows (1, 1, 3, 3) (then halves (lo, lo) / (hi, hi)), so every lane gets
+// op(op(x_r0, x_r1), op(x_r2, x_r3)), each op's operands in either order (exact: max and add are commutative).
+// Inline assembly: the compiler's builtin folds the two results into one when both inputs are the same value.  The
+// s_nops cover the VALU-write -> permlane-read hazard.
+__device__ __forceinline__ float quad_max(float v) {
+    float a = v, b = v;
+    asm("s_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\tv_max_f32 %0, %0, %1\n\tv_mov_b32 %1, %0\n\t"
+        "s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\tv_max_f32 %0, %0, %1"
+        : "+v"(a), "+v"(b));
+    return a;
+}
+__device__ __forceinline__ float quad_sum(float v) {
+    float a = v, b = v;
+    asm("s_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\tv_add_f32 %0, %0, %1\n\tv_mov_b32 %1, %0\n\t"
+        "s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\tv_add_f32 %0, %0, %1"
+        : "+v"(a), "+v"(b));
+    return a;
+}
+
 // ------------------------------------------------------------------------------------------------ quantizers
 // One row per wave: lane l holds values 4l .. 4l+3 (a 32-value block = 8 lanes).
 

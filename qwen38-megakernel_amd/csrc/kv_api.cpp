@@ -407,7 +407,7 @@ int mk_kv_attend(void * h, int layer0, int n_layers, int n_seq, const int * seqs
         a.S = s.S;
         a.T = T;
         a.R = GQA * T;
-        a.RP = a.R <= 8 ? 8 : a.R <= 16 ? 16 : a.R <= 24 ? 24 : 48; // 8-row groups: 1, 2, 3 or 6 per kernel
+        a.RP = a.R <= 8 ? 8 : 16; // one 8-row group (T = 1), else batches of 16 rows
         a.nseq = n_seq;
         int seg_total = 0;
         for (int i = 0; i < n_seq; i++) {
@@ -447,7 +447,8 @@ int mk_kv_attend(void * h, int layer0, int n_layers, int n_seq, const int * seqs
                 b.sd[i].item0 = item;
                 item += b.nl * NKV * b.sd[i].nseg;
             }
-            b.n_items = item;
+            b.n_base = item;
+            b.n_items = item * ((a.R + a.RP - 1) / a.RP);
             b.q = q + (size_t) l * n_seq * T * NH * HD;
             b.out = out + (size_t) l * n_seq * T * NH * HD;
             b.part = static_cast<float *>(s.part) + item_base * a.R * HD;

@@ -352,7 +352,12 @@ __device__ __forceinline__ void compute_tile(WaveState<NP> & st, const half8 * s
     // partition only: deterministic.
     constexpr float RESCALE_LOG2 = 8.f;
     const bool full = p0 + ATP - 1 <= st.lim_min; // every position of the tile visible to every row (uniform)
-    float p[NP][8], alpha[NP];
+    // B operands of the two 16-position groups G: (P, 0) in even columns, (0, P) in odd ones; built per row group
+    // right after its softmax so that only the packed fp16 P stays live
+    const unsigned odd = n & 1;
+    const unsigned sel_lo = odd ? 0x05040c0cu : 0x0c0c0504u, sel_hi = odd ? 0x07060c0cu : 0x0c0c0706u;
+    half8 pb[NP][2];
+    float alpha[NP];
     bool rescale = false;
 #pragma unroll
     for (int h = 0; h < NP; h++) {
@@ -369,42 +374,30 @@ __device__ __forceinline__ void compute_tile(WaveState<NP> & st, const half8 * s
         const float mold = st.m[h];
         const float mnew = mx > mold + RESCALE_LOG2 ? mx : mold; // (mold = -inf: any finite mx)
         float al = 1.f, ps = 0.f;
+        float p[8];
         if (mnew != -INFINITY) {
             al = mold == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mold - mnew);
 #pragma unroll
             for (int e = 0; e < 8; e++) {
-                p[h][e] = __builtin_amdgcn_exp2f(t[e] - mnew);
-                ps += p[h][e];
+                p[e] = __builtin_amdgcn_exp2f(t[e] - mnew);
+                ps += p[e];
             }
         } else {
 #pragma unroll
-            for (int e = 0; e < 8; e++) p[h][e] = 0.f;
+            for (int e = 0; e < 8; e++) p[e] = 0.f;
         }
         ps = quad_sum(ps);
         st.l[h] = __builtin_fmaf(st.l[h], al, ps);
         st.m[h] = mnew;
         alpha[h] = al;
         rescale |= al != 1.f && mold != -INFINITY; // (O is still zero before the first visible tile)
-    }
-    if (__any(rescale)) { // alpha == 1 exactly leaves O unchanged: the skip is exact
-#pragma unroll
-        for (int h = 0; h < NP; h++)
-#pragma unroll
-            for (int b = 0; b < 8; b++) st.acc[h][b] *= alpha[h];
-    }
-    // ---- B operands of the two 16-position groups G: (P, 0) in even columns, (0, P) in odd ones
-    const unsigned odd = n & 1;
-    const unsigned sel_lo = odd ? 0x05040c0cu : 0x0c0c0504u, sel_hi = odd ? 0x07060c0cu : 0x0c0c0706u;
-    half8 pb[NP][2];
-#pragma unroll
-    for (int h = 0; h < NP; h++)
 #pragma unroll
         for (int G = 0; G < 2; G++)
 #pragma unroll
             for (int k = 0; k < 2; k++) {
                 half2v x2;
-                x2[0] = (_Float16) p[h][4 * G + 2 * k];
-                x2[1] = (_Float16) p[h][4 * G + 2 * k + 1];
+                x2[0] = (_Float16) p[4 * G + 2 * k];
+                x2[1] = (_Float16) p[4 * G + 2 * k + 1];
                 const unsigned x = as_u(x2);
                 const half2v y0 = as_h2(perm_b32(x, 0u, sel_lo)), y1 = as_h2(perm_b32(x, 0u, sel_hi));
                 pb[h][G][4 * k] = y0[0];
@@ -412,6 +405,13 @@ __device__ __forceinline__ void compute_tile(WaveState<NP> & st, const half8 * s
                 pb[h][G][4 * k + 2] = y1[0];
                 pb[h][G][4 * k + 3] = y1[1];
             }
+    }
+    if (__any(rescale)) { // alpha == 1 exactly leaves O unchanged: the skip is exact
+#pragma unroll
+        for (int h = 0; h < NP; h++)
+#pragma unroll
+            for (int b = 0; b < 8; b++) st.acc[h][b] *= alpha[h];
+    }
     // ---- O += P V: block b = dims 16 m + 2 b, + 1 of the lane's V row m (nibble word b / 4, values 2 (b % 4), + 1)
     half2v dv[8];
 #pragma unroll
@@ -460,6 +460,9 @@ __device__ __forceinline__ void set_prio(int left) {
 }
 
 // ------------------------------------------------------------------------------------------------ the kernel
+// More than 16 query rows (T >= 3) run as batches of 16 rows: work item = (row batch, sequence, layer, kv head,
+// segment), batch-major; each batch streams the segment's tiles again with the two-group kernel, so no kernel holds
+// more than two groups of accumulators, and every row sees the same slices, tile arithmetic and merge whatever T.
 template <int NP, int KB, int VB>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NP == 1 ? 2 : 1, NP == 1 ? 2 : 1))) void k_attn(AttnArgs a) {
     constexpr int RP = 8 * NP; // query rows held (the padding rows are zero)
@@ -471,7 +474,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NP == 1 ? 2
     const unsigned lds0 = (unsigned) (size_t) (__attribute__((address_space(3))) uint8_t *) smem;
     const unsigned st_lds = (unsigned) __builtin_amdgcn_readfirstlane(lds0 + wv * STAGE_BYTES);
     half8 * const sQ = reinterpret_cast<half8 *>(smem + ATTN_LDS); // [RP][256] fp16, chunk-swizzled (qchunk)
-    for (int item = blockIdx.x; item < a.n_items; item += gridDim.x) {
+    for (int bitem = blockIdx.x; bitem < a.n_items; bitem += gridDim.x) {
+        const int batch = bitem / a.n_base, item = bitem - batch * a.n_base, row0 = RP * batch;
         int si = 0;
 #pragma unroll
         for (int i = 1; i < 8; i++)
@@ -517,8 +521,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NP == 1 ? 2
         // ---- queries: FWHT when K is stored rotated, * 1/16, fp16 (qwen38_mk.cu:2873-2880), rows r = hh T + t
         for (int r = wv; r < RP; r += AWAVES) {
             half2v o0 = {(_Float16) 0.f, (_Float16) 0.f}, o1 = o0;
-            if (r < a.R) {
-                const int hh = r / T, t = r % T;
+            if (row0 + r < a.R) {
+                const int hh = (row0 + r) / T, t = (row0 + r) % T;
                 const float4 x = *reinterpret_cast<const float4 *>(a.q + (((size_t) (l * a.nseq + si) * T + t) * NH + GQA * g + hh) * HD + 4 * lane);
                 float v[4] = {x.x, x.y, x.z, x.w};
                 if ((a.krot >> (a.layer0 + l)) & 1u) fwht256_w64(v);
@@ -534,7 +538,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NP == 1 ? 2
         for (int h = 0; h < NP; h++) {
             st.m[h] = -INFINITY;
             st.l[h] = 0.f;
-            const int row = 8 * h + (n >> 1);
+            const int row = row0 + 8 * h + (n >> 1);
             st.lim[h] = row < a.R ? L - T + row % T : -1;
 #pragma unroll
             for (int b = 0; b < 8; b++) st.acc[h][b] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -580,7 +584,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NP == 1 ? 2
             }
         }
         __syncthreads();
-        const int R = a.R;
+        const int R = a.R, RB = min(RP, R - row0); // rows of this batch
         constexpr int NPASS = (NP + 1) / 2;
 #pragma unroll
         for (int ps = 0; ps < NPASS; ps++) {
@@ -599,7 +603,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NP == 1 ? 2
                 }
             }
             __syncthreads();
-            const int nrow = min(16, R - 16 * ps);
+            const int nrow = min(16, RB - 16 * ps);
             for (int idx = threadIdx.x; idx < nrow * (HD / 4); idx += 256) {
                 const int r16 = idx / (HD / 4), c4 = idx % (HD / 4);
                 const float * src = reinterpret_cast<const float *>(smem) + r16 * OLD + 4 * c4;
@@ -612,11 +616,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NP == 1 ? 2
                     y.z += z.z;
                     y.w += z.w;
                 }
-                *reinterpret_cast<float4 *>(a.part + ((size_t) item * R + 16 * ps + r16) * HD + 4 * c4) = y;
+                *reinterpret_cast<float4 *>(a.part + ((size_t) item * R + row0 + 16 * ps + r16) * HD + 4 * c4) = y;
             }
             if (ps + 1 < NPASS) __syncthreads();
         }
-        if (threadIdx.x < R) {
+        if (threadIdx.x < RB) {
             const int row = threadIdx.x;
             const float M = fmaxf(fmaxf(s_m[row], s_m[RP + row]), fmaxf(s_m[2 * RP + row], s_m[3 * RP + row]));
             float lsum = 0.f;
@@ -625,7 +629,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NP == 1 ? 2
                 const float ew = s_m[w * RP + row] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(s_m[w * RP + row] - M);
                 lsum += ew * s_l[w * RP + row];
             }
-            a.ml[(size_t) item * R + row] = make_float2(M, lsum);
+            a.ml[(size_t) item * R + row0 + row] = make_float2(M, lsum);
         }
         __syncthreads(); // the LDS is reused by the next item
     }
@@ -828,8 +832,6 @@ hipError_t launch_attn(const AttnArgs & a, int kb, int vb, int max_blocks, hipSt
     const int np = a.RP / 8;
     if (np == 1) k = pick<1>(kb, vb);
     else if (np == 2) k = pick<2>(kb, vb);
-    else if (np == 3) k = pick<3>(kb, vb);
-    else if (np == 6) k = pick<6>(kb, vb);
     if (!k) return hipErrorInvalidValue;
     static thread_local const void * configured[128];
     static thread_local int n_configured = 0;

@@ -19,9 +19,10 @@ struct AttnArgs {
     StoreLayout S;
     int layer0;          // first slot of the launch
     int nl;              // layers in the launch (all with the same K/V bits)
-    int T, R, RP;        // query tokens, query rows per kv head (6 T), rows held in 8-row groups (8, 16, 24 or 48)
+    int T, R, RP;        // query tokens, query rows per kv head (6 T), rows per batch: 8 (R <= 8) or 16
     int nseq;
-    int n_items;         // (sequence, layer, kv head, segment) work items
+    int n_base;          // (sequence, layer, kv head, segment) work items
+    int n_items;         // n_base * ceil(R / RP): every item once per row batch
     unsigned krot, vrot; // per-slot bit masks: K / V stored rotated
     SeqDesc sd[8];
     const float * q;     // [nl][nseq][T][NH][HD] queries of this launch's layers (fp32, before the 1/16 scale)

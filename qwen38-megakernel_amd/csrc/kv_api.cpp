@@ -116,8 +116,8 @@ struct Store {
     // mk_kv_profile: a pool of event sets recorded around each call's kernels on the launch stream; a set's elapsed times
     // are read only when the pool wraps around or profiling stops, so timed back-to-back calls never wait on the host
     struct EvSet {
-        hipEvent_t e[3] = {};
-        int kind = 0; // 0 free, 1 attend (attention | combine), 2 append
+        hipEvent_t e[4] = {}; // kernel start / end: attention (0, 1) and combine (2, 3), or append (0, 1)
+        int kind = 0;         // 0 free, 1 attend, 2 append
     };
     static constexpr int NEV = 256;
     int prof = 0;
@@ -159,10 +159,10 @@ void prof_read(Store & s, Store::EvSet & es) {
     if (!es.kind) return;
     float ms = 0.f;
     if (es.kind == 1) {
-        HCK(hipEventSynchronize(es.e[2]));
+        HCK(hipEventSynchronize(es.e[3]));
         s.prof_acc[0] += 1;
         for (int i = 0; i < 2; i++) {
-            HCK(hipEventElapsedTime(&ms, es.e[i], es.e[i + 1]));
+            HCK(hipEventElapsedTime(&ms, es.e[2 * i], es.e[2 * i + 1]));
             s.prof_acc[1 + i] += ms;
         }
     } else {
@@ -183,9 +183,6 @@ Store::EvSet * prof_set(Store & s, int kind) {
     return &es;
 }
 
-void prof_mark(Store::EvSet * es, int i, hipStream_t st) {
-    if (es) HCK(hipEventRecord(es->e[i], st));
-}
 
 Store * as_store(void * h) {
     if (!h) throw std::runtime_error("null KV store handle");
@@ -385,9 +382,8 @@ int mk_kv_append(void * h, int seq, int layer0, int n_layers, int pos, int T, co
         if (dtype != 0 && dtype != 1) throw std::runtime_error("dtype: 0 fp32, 1 fp16");
         if (!k || !v) throw std::runtime_error("null K/V pointer");
         Store::EvSet * es = prof_set(s, 2);
-        prof_mark(es, 0, static_cast<hipStream_t>(stream));
-        HCK(launch_append(s.S, seq, layer0, n_layers, pos, T, k, v, dtype, static_cast<hipStream_t>(stream)));
-        prof_mark(es, 1, static_cast<hipStream_t>(stream));
+        HCK(launch_append(s.S, seq, layer0, n_layers, pos, T, k, v, dtype, static_cast<hipStream_t>(stream), es ? es->e[0] : nullptr,
+                          es ? es->e[1] : nullptr));
         s.top[seq] = std::max(s.top[seq], pos + T);
         s.n[seq] = std::max(s.n[seq], pos + T);
         return 0;
@@ -432,7 +428,6 @@ int mk_kv_attend(void * h, int layer0, int n_layers, int n_seq, const int * seqs
         s.grow(s.part, s.part_bytes, max_items * a.R * HD * sizeof(float));
         s.grow(s.ml, s.ml_bytes, max_items * a.R * sizeof(float2));
         Store::EvSet * es = prof_set(s, 1);
-        prof_mark(es, 0, st);
         size_t item_base = 0;
         std::vector<AttnArgs> groups;
         for (int l = 0; l < n_layers;) { // consecutive layers with the same K/V bits share one launch
@@ -454,13 +449,17 @@ int mk_kv_attend(void * h, int layer0, int n_layers, int n_seq, const int * seqs
             b.part = static_cast<float *>(s.part) + item_base * a.R * HD;
             b.ml = static_cast<float2 *>(s.ml) + item_base * a.R;
             item_base += (size_t) item;
-            HCK(launch_attn(b, kb, vb, s.max_blocks, st));
             groups.push_back(b);
             l = e;
         }
-        prof_mark(es, 1, st);
-        for (const AttnArgs & b : groups) HCK(launch_combine(b, st));
-        prof_mark(es, 2, st);
+        // profiling: the first launch records the start event, the last the end event (kernel timestamps)
+        const size_t ng = groups.size();
+        auto ev = [&](int i, size_t g) { return es && ((i % 2 == 0 && g == 0) || (i % 2 == 1 && g + 1 == ng)) ? es->e[i] : nullptr; };
+        for (size_t g = 0; g < ng; g++) {
+            const AttnArgs & b = groups[g];
+            HCK(launch_attn(b, s.S.side[b.layer0][0].bits, s.S.side[b.layer0][1].bits, s.max_blocks, st, ev(0, g), ev(1, g)));
+        }
+        for (size_t g = 0; g < ng; g++) HCK(launch_combine(groups[g], st, ev(2, g), ev(3, g)));
         return 0;
     });
 }

@@ -794,11 +794,11 @@ __global__ __launch_bounds__(256) void k_combine_split(AttnArgs a) {
         make_float4(y.x / dd, y.y / dd, y.z / dd, y.w / dd);
 }
 
-hipError_t launch_combine(const AttnArgs & a, hipStream_t st) {
+hipError_t launch_combine(const AttnArgs & a, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {
     const unsigned rows = (unsigned) (a.nl * a.nseq * NKV * a.R);
     const unsigned vrot = (a.vrot >> a.layer0) & ((a.nl >= 32 ? 0u : 1u << a.nl) - 1u);
-    if (vrot) hipLaunchKernelGGL(k_combine, dim3(rows), dim3(256), 0, st, a);
-    else hipLaunchKernelGGL(k_combine_split, dim3(4 * rows), dim3(256), 0, st, a);
+    if (vrot) hipExtLaunchKernelGGL(k_combine, dim3(rows), dim3(256), 0, st, ev0, ev1, 0, a);
+    else hipExtLaunchKernelGGL(k_combine_split, dim3(4 * rows), dim3(256), 0, st, ev0, ev1, 0, a);
     return hipGetLastError();
 }
 
@@ -827,7 +827,7 @@ static AttnKernel pick(int kb, int vb) {
 #undef QKV_VB
 }
 
-hipError_t launch_attn(const AttnArgs & a, int kb, int vb, int max_blocks, hipStream_t st) {
+hipError_t launch_attn(const AttnArgs & a, int kb, int vb, int max_blocks, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {
     AttnKernel k = nullptr;
     const int np = a.RP / 8;
     if (np == 1) k = pick<1>(kb, vb);
@@ -845,7 +845,7 @@ hipError_t launch_attn(const AttnArgs & a, int kb, int vb, int max_blocks, hipSt
     }
     int blocks = a.n_items;
     if (max_blocks > 0 && blocks > max_blocks) blocks = max_blocks;
-    hipLaunchKernelGGL(k, dim3(blocks), dim3(256), lds, st, a);
+    hipExtLaunchKernelGGL(k, dim3(blocks), dim3(256), lds, st, ev0, ev1, 0, a);
     return hipGetLastError();
 }
 

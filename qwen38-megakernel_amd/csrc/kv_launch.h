@@ -1,6 +1,7 @@
 // Kernel launchers of the KV path (defined in kv_store.hip / kv_attn*.hip), called by the C-ABI host code.
 #pragma once
 #include <hip/hip_runtime.h>
+#include <hip/hip_ext.h>
 #include "kv_layout.h"
 
 namespace qkv {
@@ -43,10 +44,13 @@ constexpr int MAX_SEG = 128;
 constexpr int STAGE_BYTES = 2 * 32 * 256 + 1024; // one 32-position tile, widest format (q8 K and V) + its scales
 constexpr int ATTN_LDS = AWAVES * STAGE_BYTES;   // one stage per wave (+ the query rows: RP * 512 bytes)
 
+// ev0 / ev1: optional events recorded at the kernel's own start and end (hipExtLaunchKernelGGL: the dispatch packet's
+// timestamps, the same the profiler reads), for the store's kernel timing
 hipError_t launch_append(const StoreLayout & S, int seq, int layer0, int nl, int pos, int T, const void * k, const void * v, int f16,
-                         hipStream_t st);
+                         hipStream_t st, hipEvent_t ev0 = nullptr, hipEvent_t ev1 = nullptr);
 hipError_t launch_ring_refill(const StoreLayout & S, int seq, int nl, int p0, int p1, hipStream_t st);
-hipError_t launch_attn(const AttnArgs & a, int kb, int vb, int max_blocks, hipStream_t st);
-hipError_t launch_combine(const AttnArgs & a, hipStream_t st);
+hipError_t launch_attn(const AttnArgs & a, int kb, int vb, int max_blocks, hipStream_t st, hipEvent_t ev0 = nullptr,
+                       hipEvent_t ev1 = nullptr);
+hipError_t launch_combine(const AttnArgs & a, hipStream_t st, hipEvent_t ev0 = nullptr, hipEvent_t ev1 = nullptr);
 
 } // namespace qkv

@@ -125,9 +125,9 @@ __global__ __launch_bounds__(256) void k_ring_refill(StoreLayout S, int seq, int
 }
 
 hipError_t launch_append(const StoreLayout & S, int seq, int layer0, int nl, int pos, int T, const void * k, const void * v, int f16,
-                         hipStream_t st) {
+                         hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {
     const int waves = T * nl * NKV * 2;
-    hipLaunchKernelGGL(k_append, dim3((waves + 3) / 4), dim3(256), 0, st, S, seq, layer0, nl, pos, T, k, v, f16);
+    hipExtLaunchKernelGGL(k_append, dim3((waves + 3) / 4), dim3(256), 0, st, ev0, ev1, 0, S, seq, layer0, nl, pos, T, k, v, f16);
     return hipGetLastError();
 }
 

@@ -460,9 +460,10 @@ __device__ __forceinline__ void set_prio(int left) {
 }
 
 // ------------------------------------------------------------------------------------------------ the kernel
-// More than 16 query rows (T >= 3) run as batches of 16 rows: work item = (row batch, sequence, layer, kv head,
-// segment), batch-major; each batch streams the segment's tiles again with the two-group kernel, so no kernel holds
-// more than two groups of accumulators, and every row sees the same slices, tile arithmetic and merge whatever T.
+// More than 16 query rows (T >= 3) run as batches of 16 rows: work item = (sequence, layer, kv head, segment, row
+// batch), batch-minor; each batch streams the segment's tiles again with the two-group kernel, so no kernel holds more
+// than two groups of accumulators, and every row sees the same slices, tile arithmetic and merge whatever T.  The
+// batches of a segment run side by side, so its second and third reads mostly hit the last-level cache.
 template <int NP, int KB, int VB>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NP == 1 ? 2 : 1, NP == 1 ? 2 : 1))) void k_attn(AttnArgs a) {
     constexpr int RP = 8 * NP; // query rows held (the padding rows are zero)
@@ -475,7 +476,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NP == 1 ? 2
     const unsigned st_lds = (unsigned) __builtin_amdgcn_readfirstlane(lds0 + wv * STAGE_BYTES);
     half8 * const sQ = reinterpret_cast<half8 *>(smem + ATTN_LDS); // [RP][256] fp16, chunk-swizzled (qchunk)
     for (int bitem = blockIdx.x; bitem < a.n_items; bitem += gridDim.x) {
-        const int batch = bitem / a.n_base, item = bitem - batch * a.n_base, row0 = RP * batch;
+        const int nb = a.n_items / a.n_base, item = bitem / nb, batch = bitem - item * nb, row0 = RP * batch;
         int si = 0;
 #pragma unroll
         for (int i = 1; i < 8; i++)

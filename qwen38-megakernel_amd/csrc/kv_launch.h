@@ -23,7 +23,7 @@ struct AttnArgs {
     int T, R, RP;        // query tokens, query rows per kv head (6 T), rows per batch: 8 (R <= 8) or 16
     int nseq;
     int n_base;          // (sequence, layer, kv head, segment) work items
-    int n_items;         // n_base * ceil(R / RP): every item once per row batch
+    int n_items;         // n_base * ceil(R / RP): every item once per row batch (batch-minor)
     unsigned krot, vrot; // per-slot bit masks: K / V stored rotated
     SeqDesc sd[8];
     const float * q;     // [nl][nseq][T][NH][HD] queries of this launch's layers (fp32, before the 1/16 scale)

@@ -236,6 +236,35 @@ def cpu_baseline(qkv, seconds=10.0):
                       f"fp16-valued operands, {n} repetitions in {el:.1f} s with {threads} threads (kv_oracle.c)"}
 
 
+def cpu_extras(seconds=3.0):
+    """The oracle on host cores for config 1 (q8 attention over 4,096 positions, 4 kv heads x 6 rows) and config 2
+    (one append step: 16 layers x 4 kv heads x 8 positions x K/V rows, FWHT on K, K 5-bit + V 6-bit + q8 ring copies)."""
+    from oracle import oracle as o
+    threads = max(1, min(16, os.cpu_count() or 1))
+    rng = np.random.default_rng(0)
+    L = 4096
+    K = np.stack([o.dequant_rows(*o.store_rows(rng.standard_normal((L, HD)).astype(np.float32), 0, 8, ring=False)[:2], 8)
+                  for _ in range(NKV)])
+    V = np.stack([o.dequant_rows(*o.store_rows(rng.standard_normal((L, HD)).astype(np.float32), 0, 8, ring=False)[:2], 8)
+                  for _ in range(NKV)])
+    q = np.stack([np.stack([o.q_prep(x, 0) for x in rng.standard_normal((6, HD)).astype(np.float32)]) for _ in range(NKV)])
+    n, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        o.attn_heads(q, K, V, 1, threads)
+        n += 1
+    c1 = L * n / (time.perf_counter() - t0)
+    rows = rng.standard_normal((16 * NKV * 8, HD)).astype(np.float32)
+    n, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        o.store_rows(rows, 1, 5, ring=True, threads=threads)
+        o.store_rows(rows, 0, 6, ring=True, threads=threads)
+        n += 1
+    us = (time.perf_counter() - t0) / n * 1e6
+    return {"cfg1_attention": {"value": c1, "unit": "KV positions/s", "cores": threads, "kind": "port"},
+            "cfg2_append": {"value": us, "unit": "us/step", "cores": threads, "kind": "port",
+                            "sample": "512 K rows (FWHT, 5-bit) + 512 V rows (6-bit), each with its q8 ring copy"}}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -277,6 +306,8 @@ def main():
         extra["cfg5"] = bench_cfg5(torch, qkv, args.steps, args.warmup)
     c3 = extra.get("cfg3")
     cpu = None if args.no_cpu or 3 not in cfgs else cpu_baseline(qkv, args.cpu_seconds)
+    if cpu:
+        cpu["other_configs"] = cpu_extras()
     roof = None
     if c3:
         ach = c3["attn_kernel_gbps"] * 1e9

@@ -88,6 +88,20 @@ int mk_kv_state_digest(void * h, int seq, unsigned long long * out, int cap);
  * row bytes.  Test and park/unpark helper (host_store.cu:80-160 copies the same rows). */
 int mk_kv_read_rows(void * h, int seq, int layer, int w, int g, int p0, int n, int ring, void * vals, unsigned short * scales);
 
+/* Write n logical rows back into the store (the unpark half of host_store.cu:80-160's park/unpark copies): main-store
+ * rows (ring = 0; vals n * 32 * bits bytes) or window-ring rows (ring = 1; n * 256 bytes, n <= ring rows), scales
+ * n * 8 fp16, from host memory.  The sequence's stored length grows to cover them.  Returns 0. */
+int mk_kv_write_rows(void * h, int seq, int layer, int w, int g, int p0, int n, int ring, const void * vals, const unsigned short * scales);
+
+/* Window-ring snapshots for exact checkpoint reuse (the MK_EXACT ring copies of a checkpoint save / restore,
+ * ck_pool.cu:39-42, 135-194, 268-296).  mk_kv_ring_snapshot copies every ring of sequence seq (with a header holding
+ * the store layout and the sequence's position) to dst (host or device memory) and returns the byte count; dst NULL
+ * or cap too small returns the count needed and copies nothing.  mk_kv_ring_restore puts a snapshot back and rewinds
+ * the sequence to pos (<= the snapshot's position): ring rows the snapshot holds are restored bit for bit, older
+ * window rows are refilled from the main rows as mk_kv_rewind does.  Both synchronise the device. */
+long long mk_kv_ring_snapshot(void * h, int seq, void * dst, long long cap);
+int mk_kv_ring_restore(void * h, int seq, int pos, const void * src, long long bytes);
+
 /* Knobs: "max_blocks" caps the attention grid (0: one workgroup per work item); results never depend on it. */
 int mk_kv_config(void * h, const char * key, long long value);
 

@@ -517,6 +517,108 @@ int mk_kv_read_rows(void * h, int seq, int layer, int w, int g, int p0, int n, i
     });
 }
 
+int mk_kv_write_rows(void * h, int seq, int layer, int w, int g, int p0, int n, int ring, const void * vals, const unsigned short * scales) {
+    return guarded([&] {
+        Store & s = *as_store(h);
+        check_seq(s, seq);
+        check_layers(s, layer, 1);
+        if (w < 0 || w > 1 || g < 0 || g >= NKV) throw std::runtime_error("side / kv head out of range");
+        if (p0 < 0 || n < 0 || p0 + n > s.ctx) throw std::runtime_error("rows outside 0 .. ctx-1");
+        if (!vals || !scales) throw std::runtime_error("null rows / scales");
+        const SideLayout & sd = s.S.side[layer][w];
+        HCK(hipDeviceSynchronize());
+        if (ring) {
+            if (!sd.ring) throw std::runtime_error("this side has no window ring");
+            if (n > s.kvrc) throw std::runtime_error("more rows than the ring holds");
+            for (int i = 0; i < n; i++) {
+                const size_t r = (size_t) (seq * NKV + g) * s.kvrc + (p0 + i) % s.kvrc;
+                HCK(hipMemcpy(sd.ring + r * HD, static_cast<const uint8_t *>(vals) + (size_t) i * HD, HD, hipMemcpyHostToDevice));
+                HCK(hipMemcpy(sd.rsc + r * 8, scales + (size_t) i * 8, 16, hipMemcpyHostToDevice));
+            }
+        } else {
+            const size_t rb = (size_t) row_bytes(sd.bits);
+            for (int p = p0; p < p0 + n;) {
+                const int cnt = std::min(p0 + n - p, s.page - p % s.page);
+                const size_t r = s.main_row(seq, g, p);
+                HCK(hipMemcpy(sd.vals + r * rb, static_cast<const uint8_t *>(vals) + (size_t) (p - p0) * rb, (size_t) cnt * rb, hipMemcpyHostToDevice));
+                HCK(hipMemcpy(sd.scs + r * 8, scales + (size_t) (p - p0) * 8, (size_t) cnt * 16, hipMemcpyHostToDevice));
+                p += cnt;
+            }
+        }
+        s.n[seq] = std::max(s.n[seq], p0 + n);
+        s.top[seq] = std::max(s.top[seq], p0 + n);
+        return 0;
+    });
+}
+
+// ring snapshot: header of 8 int64 [magic, version 1, kvrc, ring sides, position, n_layers, 0, 0], then per (slot, side)
+// with a ring, in slot order, K before V: the sequence's ring values [NKV][kvrc][256] and scales [NKV][kvrc][8] fp16
+static constexpr long long RING_SNAP_MAGIC = 0x4d4b52494e47ll; // "MKRING"
+static long long ring_snap_bytes(const Store & s, int & sides) {
+    sides = 0;
+    for (int l = 0; l < s.n_layers; l++)
+        for (int w = 0; w < 2; w++) sides += s.S.side[l][w].ring != nullptr;
+    return 64 + (long long) sides * NKV * s.kvrc * (HD + 16);
+}
+
+long long mk_kv_ring_snapshot(void * h, int seq, void * dst, long long cap) {
+    long long r = -1;
+    const int st = guarded([&] {
+        Store & s = *as_store(h);
+        check_seq(s, seq);
+        int sides = 0;
+        const long long need = ring_snap_bytes(s, sides);
+        r = need;
+        if (!dst || cap < need) return 0;
+        HCK(hipDeviceSynchronize());
+        const long long hdr[8] = {RING_SNAP_MAGIC, 1, s.kvrc, sides, s.n[seq], s.n_layers, 0, 0};
+        HCK(hipMemcpy(dst, hdr, sizeof hdr, hipMemcpyDefault));
+        uint8_t * o = static_cast<uint8_t *>(dst) + 64;
+        const size_t vb = (size_t) NKV * s.kvrc * HD, sb = (size_t) NKV * s.kvrc * 16;
+        for (int l = 0; l < s.n_layers; l++)
+            for (int w = 0; w < 2; w++) {
+                const SideLayout & sd = s.S.side[l][w];
+                if (!sd.ring) continue;
+                HCK(hipMemcpy(o, sd.ring + (size_t) seq * vb, vb, hipMemcpyDefault));
+                HCK(hipMemcpy(o + vb, reinterpret_cast<const uint8_t *>(sd.rsc) + (size_t) seq * sb, sb, hipMemcpyDefault));
+                o += vb + sb;
+            }
+        return 0;
+    });
+    return st < 0 ? -1 : r;
+}
+
+int mk_kv_ring_restore(void * h, int seq, int pos, const void * src, long long bytes) {
+    return guarded([&] {
+        Store & s = *as_store(h);
+        check_seq(s, seq);
+        int sides = 0;
+        const long long need = ring_snap_bytes(s, sides);
+        if (!src || bytes < need) throw std::runtime_error("ring snapshot too small for this store");
+        long long hdr[8];
+        HCK(hipMemcpy(hdr, src, sizeof hdr, hipMemcpyDefault));
+        if (hdr[0] != RING_SNAP_MAGIC || hdr[1] != 1) throw std::runtime_error("not a ring snapshot");
+        if (hdr[2] != s.kvrc || hdr[3] != sides || hdr[5] != s.n_layers) throw std::runtime_error("ring snapshot of a different store layout");
+        const int snap = (int) hdr[4];
+        if (pos < 0 || pos > snap) throw std::runtime_error("restore position beyond the snapshot's position");
+        if (pos > s.n[seq]) throw std::runtime_error("restore position beyond the stored rows");
+        HCK(hipDeviceSynchronize());
+        const uint8_t * in = static_cast<const uint8_t *>(src) + 64;
+        const size_t vb = (size_t) NKV * s.kvrc * HD, sb = (size_t) NKV * s.kvrc * 16;
+        for (int l = 0; l < s.n_layers; l++)
+            for (int w = 0; w < 2; w++) {
+                const SideLayout & sd = s.S.side[l][w];
+                if (!sd.ring) continue;
+                HCK(hipMemcpy(sd.ring + (size_t) seq * vb, in, vb, hipMemcpyDefault));
+                HCK(hipMemcpy(reinterpret_cast<uint8_t *>(sd.rsc) + (size_t) seq * sb, in + vb, sb, hipMemcpyDefault));
+                in += vb + sb;
+            }
+        // the window rows the snapshot does not hold (positions before snap - kvrc) come from the main rows, as a rewind
+        s.top[seq] = snap;
+        return rewind_seq(s, seq, pos);
+    });
+}
+
 int mk_kv_profile(void * h, int enable, double * out, int cap) {
     return guarded([&] {
         Store & s = *as_store(h);

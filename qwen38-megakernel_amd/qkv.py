@@ -34,6 +34,9 @@ SIGNATURES = {
     "mk_state_digest": (_c_int, [_c_vp, _P_u64, _c_int]),
     "mk_kv_state_digest": (_c_int, [_c_vp, _c_int, _P_u64, _c_int]),
     "mk_kv_read_rows": (_c_int, [_c_vp, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_vp, _P_u16]),
+    "mk_kv_write_rows": (_c_int, [_c_vp, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_vp, _P_u16]),
+    "mk_kv_ring_snapshot": (_c_ll, [_c_vp, _c_int, _c_vp, _c_ll]),
+    "mk_kv_ring_restore": (_c_int, [_c_vp, _c_int, _c_int, _c_vp, _c_ll]),
     "mk_kv_config": (_c_int, [_c_vp, _c_cp, _c_ll]),
     "mk_kv_profile": (_c_int, [_c_vp, _c_int, ctypes.POINTER(ctypes.c_double), _c_int]),
     "mk_kv_window_start": (_c_int, [_c_int, _c_int]),
@@ -161,6 +164,31 @@ class KVStore:
         _check(lib().mk_kv_read_rows(self.h, seq, layer, w, g, p0, n, 1 if ring else 0, vals.ctypes.data_as(ctypes.c_void_p),
                                      sc.ctypes.data_as(_P_u16)))
         return vals, sc
+
+    def write_rows(self, seq, layer, w, g, p0, vals, scales, ring=False):
+        """Write rows (values bytes [n][row_bytes], scales uint16 [n][8]) to logical positions p0 .. p0+n-1."""
+        import numpy as np
+        vals = np.ascontiguousarray(vals, np.uint8)
+        scales = np.ascontiguousarray(scales, np.uint16)
+        _check(lib().mk_kv_write_rows(self.h, seq, layer, w, g, p0, vals.shape[0], 1 if ring else 0,
+                                      vals.ctypes.data_as(ctypes.c_void_p), scales.ctypes.data_as(_P_u16)))
+
+    def ring_snapshot(self, seq):
+        """The window rings of sequence seq as a uint8 numpy array (header + rows)."""
+        import numpy as np
+        need = lib().mk_kv_ring_snapshot(self.h, seq, None, 0)
+        if need < 0:
+            raise KVError(last_error())
+        buf = np.zeros(need, np.uint8)
+        got = lib().mk_kv_ring_snapshot(self.h, seq, buf.ctypes.data_as(ctypes.c_void_p), need)
+        if got != need:
+            raise KVError(last_error())
+        return buf
+
+    def ring_restore(self, seq, pos, snap):
+        import numpy as np
+        snap = np.ascontiguousarray(snap, np.uint8)
+        _check(lib().mk_kv_ring_restore(self.h, seq, pos, snap.ctypes.data_as(ctypes.c_void_p), snap.size))
 
     def profile(self, enable):
         """Start (1) / stop (0) kernel timing; returns {calls, attn_ms, combine_ms, append_ms} so far."""

@@ -66,6 +66,17 @@ int mk_kv_append(void * h, int seq, int layer0, int n_layers, int pos, int T, co
 int mk_kv_attend(void * h, int layer0, int n_layers, int n_seq, const int * seqs, const int * lens, int T, const float * q, float * out,
                  void * stream);
 
+/*
+ * mk_kv_attend followed by the combine epilogue (qwen38_mk.cu:4686-4688): out = y / (1 + exp(-gate)) with gate a
+ * device array shaped like q, and, when q32a / q32b / q32meta are given (all three or none), out in the o_proj
+ * activation units of q32_store (qwen38_mk.cu:283-307): per token row of 24 x 256 outputs, 32-value blocks
+ * j = 8 head + k quantised to int8 (amax / 127, round half away from zero); unit gi = 8 head + 2 (k / 2) + half holds
+ * 16 bytes of an even block in q32a [..][192][16] and of an odd block in q32b, and q32meta [..][192][4] = fp16 scale
+ * of the q32a / q32b block, int16 sum of the q32a / q32b half.  Shapes [n_layers][n_seq][T][...].
+ */
+int mk_kv_attend_gated(void * h, int layer0, int n_layers, int n_seq, const int * seqs, const int * lens, int T, const float * q,
+                       const float * gate, float * out, void * q32a, void * q32b, unsigned short * q32meta, void * stream);
+
 /* Rewind sequence 0 / sequence seq to position pos: ring rows refilled from the main store (ring_rewind,
  * ck_pool.cu:285-296; k_ring_refill, qwen38_mk.cu:2485-2517).  mk_truncate / mk_rewind_to replace capi.cpp:572 / 601. */
 int mk_truncate(void * h, int len);

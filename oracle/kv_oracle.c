@@ -24,6 +24,10 @@
  *   kvo_attn_chunked   the reference's split-K arithmetic (attn_dims chunks, 32-position tiles, fp16 operands,
  *                      fp32 online softmax, attn_combine); pinned against kvo_attn_exact within 2e-3.
  *   kvo_dg_hash        FNV-style row hash; pinned by hand-computed words for short inputs.
+ *   kvo_gate           y / (1 + expf(-g)) (qwen38_mk.cu:4686); pinned by closed forms (g = 0 -> y / 2, large g -> y).
+ *   kvo_q32_row        q32_store (qwen38_mk.cu:283-307) over one token's 24 x 256 output row: known answers (zero
+ *                      block, single value -> +-127, half-away-from-zero ties) and the unit layout by hand-placed
+ *                      blocks in the tests.
  */
 #include <math.h>
 #include <stdint.h>
@@ -516,4 +520,35 @@ double kvo_now(void) {
     struct timespec ts;
     clock_gettime(CLOCK_MONOTONIC, &ts);
     return (double) ts.tv_sec + 1e-9 * (double) ts.tv_nsec;
+}
+
+/* ---------------------------------------------------------------- combine epilogue (qwen38_mk.cu:4686-4688) */
+/* the sigmoid output gate */
+float kvo_gate(float y, float g) { return y / (1.0f + expf(-g)); }
+
+/* q32_store of one token's output row o[24 * 256] into the o_proj activation units (qwen38_mk.cu:283-307): block
+ * j = 8 head + k (32 values, element 32 j + i) -> amax, d = amax / 127 (IEEE division), q = roundf(v / d) (half away from
+ * zero; 0 when amax = 0); unit gi = 8 (j >> 3) + 2 ((j >> 1) & 3) + hh for the block's halves hh = i / 16: bytes
+ * (j odd ? xb : xa)[gi * 16 + i % 16]; meta[gi] = {half scale of the xa block, of the xb block, int sum of the xa
+ * half, of the xb half} (uint16 x 4). */
+void kvo_q32_row(const float * o, int8_t * xa, int8_t * xb, uint16_t * meta) {
+    for (int j = 0; j < 192; j++) {
+        const float * v = o + 32 * j;
+        float am = 0.f;
+        for (int i = 0; i < 32; i++) am = fmaxf(am, fabsf(v[i]));
+        const float d = am / 127.0f;
+        int qs[2] = {0, 0};
+        const int part = j & 1, gi0 = 8 * (j >> 3) + 2 * ((j >> 1) & 3);
+        for (int i = 0; i < 32; i++) {
+            const int q = am == 0.0f ? 0 : (int) roundf(v[i] / d);
+            const int gi = gi0 + i / 16;
+            (part ? xb : xa)[gi * 16 + i % 16] = (int8_t) q;
+            qs[i / 16] += q;
+        }
+        for (int hh = 0; hh < 2; hh++) {
+            const int gi = gi0 + hh;
+            meta[gi * 4 + part] = kvo_f2h(d);
+            meta[gi * 4 + 2 + part] = (uint16_t) (int16_t) qs[hh];
+        }
+    }
 }

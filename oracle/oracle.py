@@ -43,6 +43,8 @@ def lib():
             "kvo_attn_heads": (ci, [vp, vp, vp, ci, ci, ci, ci, vp, ci]),
             "kvo_store_rows": (None, [vp, ci, ci, ci, vp, vp, vp, vp, ci]),
             "kvo_dg_hash": (ctypes.c_uint64, [vp, ctypes.c_size_t, ctypes.c_uint64]),
+            "kvo_gate": (cf, [cf, cf]),
+            "kvo_q32_row": (None, [vp, vp, vp, vp]),
             "kvo_row_digest": (ctypes.c_uint64, [vp, ci, vp]),
             "kvo_now": (ctypes.c_double, []),
         }
@@ -223,3 +225,20 @@ def row_digest(q, bits, s):
 
 def now():
     return lib().kvo_now()
+
+
+def gate(y, g):
+    y = np.ascontiguousarray(y, np.float32).ravel()
+    g = np.ascontiguousarray(g, np.float32).ravel()
+    return np.array([lib().kvo_gate(float(a), float(b)) for a, b in zip(y, g)], np.float32)
+
+
+def q32_row(o):
+    """One token's output row o [24 * 256] -> (xa [192][16] int8, xb [192][16] int8, meta [192][4] uint16)."""
+    o = np.ascontiguousarray(o, np.float32).ravel()
+    assert o.size == 24 * HD
+    xa = np.zeros((192, 16), np.int8)
+    xb = np.zeros((192, 16), np.int8)
+    meta = np.zeros((192, 4), np.uint16)
+    lib().kvo_q32_row(_p(o), _p(xa), _p(xb), _p(meta))
+    return xa, xb, meta

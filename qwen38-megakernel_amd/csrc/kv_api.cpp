@@ -390,10 +390,12 @@ int mk_kv_append(void * h, int seq, int layer0, int n_layers, int pos, int T, co
     });
 }
 
-int mk_kv_attend(void * h, int layer0, int n_layers, int n_seq, const int * seqs, const int * lens, int T, const float * q, float * out,
-                 void * stream) {
+static int attend_impl(void * h, int layer0, int n_layers, int n_seq, const int * seqs, const int * lens, int T, const float * q,
+                       const float * gate, float * out, int8_t * q32a, int8_t * q32b, uint16_t * q32m, void * stream) {
     return guarded([&] {
         Store & s = *as_store(h);
+        if ((q32a != nullptr) != (q32b != nullptr) || (q32a != nullptr) != (q32m != nullptr))
+            throw std::runtime_error("the q32 outputs come as a set: a, b and meta");
         check_layers(s, layer0, n_layers);
         if (T < 1 || T > MAXT) throw std::runtime_error("T must be 1..8");
         if (n_seq < 1 || n_seq > MAX_SEQ) throw std::runtime_error("1..8 sequences per attend call");
@@ -402,6 +404,7 @@ int mk_kv_attend(void * h, int layer0, int n_layers, int n_seq, const int * seqs
         AttnArgs a{};
         a.S = s.S;
         a.T = T;
+        a.gate = gate;
         a.R = GQA * T;
         a.RP = a.R <= 8 ? 8 : 16; // one 8-row group (T = 1), else batches of 16 rows
         a.nseq = n_seq;
@@ -446,6 +449,12 @@ int mk_kv_attend(void * h, int layer0, int n_layers, int n_seq, const int * seqs
             b.n_items = item * ((a.R + a.RP - 1) / a.RP);
             b.q = q + (size_t) l * n_seq * T * NH * HD;
             b.out = out + (size_t) l * n_seq * T * NH * HD;
+            if (gate) b.gate = gate + (size_t) l * n_seq * T * NH * HD;
+            if (q32a) {
+                b.q32a = q32a + (size_t) l * n_seq * T * 192 * 16;
+                b.q32b = q32b + (size_t) l * n_seq * T * 192 * 16;
+                b.q32m = q32m + (size_t) l * n_seq * T * 192 * 4;
+            }
             b.part = static_cast<float *>(s.part) + item_base * a.R * HD;
             b.ml = static_cast<float2 *>(s.ml) + item_base * a.R;
             item_base += (size_t) item;
@@ -461,6 +470,22 @@ int mk_kv_attend(void * h, int layer0, int n_layers, int n_seq, const int * seqs
         }
         for (size_t g = 0; g < ng; g++) HCK(launch_combine(groups[g], st, ev(2, g), ev(3, g)));
         return 0;
+    });
+}
+
+int mk_kv_attend(void * h, int layer0, int n_layers, int n_seq, const int * seqs, const int * lens, int T, const float * q, float * out,
+                 void * stream) {
+    return attend_impl(h, layer0, n_layers, n_seq, seqs, lens, T, q, nullptr, out, nullptr, nullptr, nullptr, stream);
+}
+
+int mk_kv_attend_gated(void * h, int layer0, int n_layers, int n_seq, const int * seqs, const int * lens, int T, const float * q,
+                       const float * gate, float * out, void * q32a, void * q32b, unsigned short * q32meta, void * stream) {
+    return guarded([&] {
+        if (!gate) throw std::runtime_error("null gate pointer");
+        const int r = attend_impl(h, layer0, n_layers, n_seq, seqs, lens, T, q, gate, out, static_cast<int8_t *>(q32a),
+                                  static_cast<int8_t *>(q32b), q32meta, stream);
+        if (r < 0) throw std::runtime_error(g_err); // (the message attend_impl left)
+        return r;
     });
 }
 

@@ -710,7 +710,38 @@ __global__ __launch_bounds__(256) void k_combine(AttnArgs a) {
     float v[4] = {y.x / dd, y.y / dd, y.z / dd, y.w / dd};
     if ((a.vrot >> (a.layer0 + l)) & 1u) fwht256_w64(v);
     const int h = GQA * g + r / T, t = r % T;
-    *reinterpret_cast<float4 *>(a.out + (((size_t) (l * a.nseq + si) * T + t) * NH + h) * HD + 4 * lane) = make_float4(v[0], v[1], v[2], v[3]);
+    const size_t trow = (size_t) (l * a.nseq + si) * T + t; // the token's row of 24 x 256 outputs
+    if (a.gate) { // the sigmoid output gate (qwen38_mk.cu:4686)
+        const float4 gt = *reinterpret_cast<const float4 *>(a.gate + (trow * NH + h) * HD + 4 * lane);
+        v[0] = v[0] / (1.0f + expf(-gt.x));
+        v[1] = v[1] / (1.0f + expf(-gt.y));
+        v[2] = v[2] / (1.0f + expf(-gt.z));
+        v[3] = v[3] / (1.0f + expf(-gt.w));
+    }
+    *reinterpret_cast<float4 *>(a.out + (trow * NH + h) * HD + 4 * lane) = make_float4(v[0], v[1], v[2], v[3]);
+    if (a.q32a) {
+        // q32_store (qwen38_mk.cu:283-307): block k = lane / 8 of the head's 8 blocks of 32 (j = 8 h + k), amax / 127,
+        // round half away from zero; unit gi = 8 h + 2 (k / 2) + half, bytes of the even blocks in a, odd ones in b
+        float am = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+        am = fmaxf(am, shfl_xor(am, 1));
+        am = fmaxf(am, shfl_xor(am, 2));
+        am = fmaxf(am, shfl_xor(am, 4));
+        const float d = am / 127.0f;
+        int qv[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) qv[k] = am == 0.0f ? 0 : (int) roundf(v[k] / d);
+        const int k8 = lane >> 3, part = k8 & 1, hh = (lane >> 2) & 1;
+        const size_t gi = trow * 192 + 8 * h + 2 * (k8 >> 1) + hh;
+        const unsigned packed = (qv[0] & 0xff) | (qv[1] & 0xff) << 8 | (qv[2] & 0xff) << 16 | (unsigned) (qv[3] & 0xff) << 24;
+        *reinterpret_cast<unsigned *>((part ? a.q32b : a.q32a) + gi * 16 + 4 * (lane & 3)) = packed;
+        int sum = qv[0] + qv[1] + qv[2] + qv[3];
+        sum += __shfl_xor(sum, 1, 64);
+        sum += __shfl_xor(sum, 2, 64);
+        if ((lane & 3) == 0) {
+            a.q32m[gi * 4 + part] = f2h_bits(d);
+            a.q32m[gi * 4 + 2 + part] = (uint16_t) (int16_t) sum;
+        }
+    }
 }
 
 // The same merge for launches without rotated V, spread wider: one workgroup per (output row, 64-dim quarter).  Lane
@@ -798,7 +829,7 @@ __global__ __launch_bounds__(256) void k_combine_split(AttnArgs a) {
 hipError_t launch_combine(const AttnArgs & a, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {
     const unsigned rows = (unsigned) (a.nl * a.nseq * NKV * a.R);
     const unsigned vrot = (a.vrot >> a.layer0) & ((a.nl >= 32 ? 0u : 1u << a.nl) - 1u);
-    if (vrot) hipExtLaunchKernelGGL(k_combine, dim3(rows), dim3(256), 0, st, ev0, ev1, 0, a);
+    if (vrot || a.gate || a.q32a) hipExtLaunchKernelGGL(k_combine, dim3(rows), dim3(256), 0, st, ev0, ev1, 0, a);
     else hipExtLaunchKernelGGL(k_combine_split, dim3(4 * rows), dim3(256), 0, st, ev0, ev1, 0, a);
     return hipGetLastError();
 }

@@ -28,6 +28,10 @@ struct AttnArgs {
     SeqDesc sd[8];
     const float * q;     // [nl][nseq][T][NH][HD] queries of this launch's layers (fp32, before the 1/16 scale)
     float * out;         // [nl][nseq][T][NH][HD]
+    const float * gate;  // optional [nl][nseq][T][NH][HD]: out = y / (1 + exp(-gate))
+    int8_t * q32a;       // optional o_proj activation units of out: [nl][nseq][T][192][16] int8 (even blocks)
+    int8_t * q32b;       // ... (odd blocks)
+    uint16_t * q32m;     // ... [nl][nseq][T][192][4]: half scales of the a / b blocks, int sums of the a / b halves
     float * part;        // [item][R][HD] per-segment partial outputs (unnormalised)
     float2 * ml;         // [item][R] per-segment (max in log2 units, sum)
 };

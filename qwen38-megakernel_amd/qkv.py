@@ -27,6 +27,8 @@ SIGNATURES = {
     "mk_kv_set_pages": (_c_int, [_c_vp, _c_int, _P_int, _c_int]),
     "mk_kv_append": (_c_int, [_c_vp, _c_int, _c_int, _c_int, _c_int, _c_int, _c_vp, _c_vp, _c_int, _c_vp]),
     "mk_kv_attend": (_c_int, [_c_vp, _c_int, _c_int, _c_int, _P_int, _P_int, _c_int, _c_vp, _c_vp, _c_vp]),
+    "mk_kv_attend_gated": (_c_int, [_c_vp, _c_int, _c_int, _c_int, _P_int, _P_int, _c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _P_u16,
+                                    _c_vp]),
     "mk_truncate": (_c_int, [_c_vp, _c_int]),
     "mk_rewind_to": (_c_int, [_c_vp, _c_int]),
     "mk_kv_rewind": (_c_int, [_c_vp, _c_int, _c_int]),
@@ -139,6 +141,14 @@ class KVStore:
         s = (ctypes.c_int * n)(*seqs)
         l = (ctypes.c_int * n)(*lens)
         _check(lib().mk_kv_attend(self.h, layer0, n_layers, n, s, l, T, q_ptr, out_ptr, stream))
+
+    def attend_gated(self, layer0, n_layers, seqs, lens, T, q_ptr, gate_ptr, out_ptr, q32a=0, q32b=0, q32meta=0, stream=0):
+        """attend + the output gate (+ the int8 o_proj units when q32a / q32b / q32meta are device pointers)."""
+        n = len(seqs)
+        s = (ctypes.c_int * n)(*seqs)
+        l = (ctypes.c_int * n)(*lens)
+        _check(lib().mk_kv_attend_gated(self.h, layer0, n_layers, n, s, l, T, q_ptr, gate_ptr, out_ptr, q32a or None, q32b or None,
+                                        ctypes.cast(q32meta, _P_u16) if q32meta else None, stream))
 
     def rewind(self, seq, pos):
         _check(lib().mk_kv_rewind(self.h, seq, pos))

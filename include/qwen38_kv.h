@@ -77,6 +77,32 @@ int mk_kv_attend(void * h, int layer0, int n_layers, int n_seq, const int * seqs
 int mk_kv_attend_gated(void * h, int layer0, int n_layers, int n_seq, const int * seqs, const int * lens, int T, const float * q,
                        const float * gate, float * out, void * q32a, void * q32b, unsigned short * q32meta, void * stream);
 
+/*
+ * The Q/K prep as a fused producer (qwen38_mk.cu:2843-2880, 2903-2910; prefill.cuh:986-1000): RMSNorm over each
+ * 256-value head row (eps 1e-6, per-slot weight) and NeoX RoPE on values 0..63 (pair i, i+32) from the store's RoPE
+ * table.  The table is [rows][32] float2 (cos, sin) in device memory: the caller's (e.g. the reference's rewritten
+ * image rows, engine.cu:30-62) via mk_kv_set_rope(h, table, rows), or with table = NULL the text table the reference
+ * builds (loader.cu:1252-1258: p * 1e7^(-2i/64) in double, rounded to float), ctx rows, built once by the store.
+ */
+int mk_kv_set_rope(void * h, const void * table, int rows);
+
+/*
+ * mk_kv_append of raw K rows: k [T][n_layers][4][256] fp32 before the k-norm / RoPE, v as for mk_kv_append (fp32),
+ * k_norm device [n_layers][256] weights; the K row of position p is normed and rotated by table row p inside the
+ * append kernel (the kv_store producer of mk_step, qwen38_mk.cu:2903-2911).
+ */
+int mk_kv_append_prep(void * h, int seq, int layer0, int n_layers, int pos, int T, const float * k, const float * v, const float * k_norm,
+                      void * stream);
+
+/*
+ * mk_kv_attend_gated on the raw q_proj output: qg device [n_layers][n_seq][T][24][512], per head 256 query values
+ * before the q-norm / RoPE followed by 256 gate values (the reference's qbuf, qwen38_mk.cu:2836, 4640);
+ * q_norm device [n_layers][256].  Query row t of a sequence of length L is rotated by table row L - T + t.  out and
+ * the optional q32 set as for mk_kv_attend_gated.  This is the attention of one mk_step slot from q_proj to o_proj.
+ */
+int mk_kv_attend_prep(void * h, int layer0, int n_layers, int n_seq, const int * seqs, const int * lens, int T, const float * qg,
+                      const float * q_norm, float * out, void * q32a, void * q32b, unsigned short * q32meta, void * stream);
+
 /* Rewind sequence 0 / sequence seq to position pos: ring rows refilled from the main store (ring_rewind,
  * ck_pool.cu:285-296; k_ring_refill, qwen38_mk.cu:2485-2517).  mk_truncate / mk_rewind_to replace capi.cpp:572 / 601. */
 int mk_truncate(void * h, int len);

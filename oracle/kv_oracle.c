@@ -28,6 +28,11 @@
  *   kvo_q32_row        q32_store (qwen38_mk.cu:283-307) over one token's 24 x 256 output row: known answers (zero
  *                      block, single value -> +-127, half-away-from-zero ties) and the unit layout by hand-placed
  *                      blocks in the tests.
+ *   kvo_rope_rows      the RoPE text table (loader.cu:1252-1258); pinned by numpy fp64 cos/sin of the same angles
+ *                      (<= 1 float ulp) and row 0 = (1, 0).
+ *   kvo_qk_prep        RMSNorm + NeoX RoPE on values 0..63 (qwen38_mk.cu:2623-2636, 2903-2910) in the HIP kernels'
+ *                      fixed arithmetic order; pinned by an fp64 numpy RMSNorm / rotate-half within 2e-6 relative,
+ *                      position 0 = RMSNorm alone, constant rows, and norm preservation of each rotated pair.
  */
 #include <math.h>
 #include <stdint.h>
@@ -551,4 +556,40 @@ void kvo_q32_row(const float * o, int8_t * xa, int8_t * xb, uint16_t * meta) {
             meta[gi * 4 + 2 + part] = (uint16_t) (int16_t) qs[hh];
         }
     }
+}
+
+/* RoPE text table rows p0 .. p0+n-1: out[(r * 32 + i) * 2 + {0, 1}] = (cos, sin) of p * 1e7^(-2i/64), computed in double
+ * and rounded to float (loader.cu:1252-1258, ROPE_BASE mk_shared.cuh:240). */
+void kvo_rope_rows(int p0, int n, float * out) {
+    for (int r = 0; r < n; r++)
+        for (int i = 0; i < 32; i++) {
+            const double th = (double) (p0 + r) * pow(10000000.0, -2.0 * i / 64.0);
+            out[(r * 32 + i) * 2] = (float) cos(th);
+            out[(r * 32 + i) * 2 + 1] = (float) sin(th);
+        }
+}
+
+/* Q/K prep of one 256-value row (qwen38_mk.cu:2903-2910, rope8 :2623-2636, EPS mk_shared.cuh:239): RMSNorm with eps
+ * 1e-6 and weights w, then pair (i, i + 32), i < 32, rotated by rc[i] = (cos, sin): first = a c - b s, second =
+ * b c + a s.  The order is the HIP kernels' (qk_prep): 64 partial sums of 4 squares as an FMA chain, an xor-butterfly
+ * over the 64 partials, 1 / sqrtf (the reference: rsqrtf, an approximation within 2 ulp), the weight folded into the
+ * scale first, the rotation as one FMA over a rounded product. */
+void kvo_qk_prep(const float * x, const float * w, const float * rc, float * out) {
+    float s[64], t[64], v[HD];
+    for (int l = 0; l < 64; l++) {
+        const float * a = x + 4 * l;
+        s[l] = fmaf(a[3], a[3], fmaf(a[2], a[2], fmaf(a[1], a[1], a[0] * a[0])));
+    }
+    for (int m = 1; m < 64; m <<= 1) {
+        for (int l = 0; l < 64; l++) t[l] = s[l] + s[l ^ m];
+        memcpy(s, t, sizeof s);
+    }
+    const float rs = 1.0f / sqrtf(s[0] / 256.0f + 1e-6f);
+    for (int i = 0; i < HD; i++) v[i] = x[i] * (rs * w[i]);
+    for (int i = 0; i < 32; i++) {
+        const float c = rc[2 * i], sn = rc[2 * i + 1], a = v[i], b = v[i + 32];
+        v[i] = fmaf(a, c, -(b * sn));
+        v[i + 32] = fmaf(a, sn, b * c);
+    }
+    memcpy(out, v, sizeof v);
 }

@@ -45,6 +45,8 @@ def lib():
             "kvo_dg_hash": (ctypes.c_uint64, [vp, ctypes.c_size_t, ctypes.c_uint64]),
             "kvo_gate": (cf, [cf, cf]),
             "kvo_q32_row": (None, [vp, vp, vp, vp]),
+            "kvo_rope_rows": (None, [ci, ci, vp]),
+            "kvo_qk_prep": (None, [vp, vp, vp, vp]),
             "kvo_row_digest": (ctypes.c_uint64, [vp, ci, vp]),
             "kvo_now": (ctypes.c_double, []),
         }
@@ -242,3 +244,21 @@ def q32_row(o):
     meta = np.zeros((192, 4), np.uint16)
     lib().kvo_q32_row(_p(o), _p(xa), _p(xb), _p(meta))
     return xa, xb, meta
+
+
+def rope_rows(p0, n):
+    """RoPE text table rows p0 .. p0+n-1 -> float32 [n][32][2] (cos, sin)."""
+    out = np.zeros((n, 32, 2), np.float32)
+    lib().kvo_rope_rows(p0, n, _p(out))
+    return out
+
+
+def qk_prep(x, w, rc):
+    """RMSNorm (weights w [256]) + RoPE (table row rc [32][2]) of one row x [256], in the HIP kernels' order."""
+    x = np.ascontiguousarray(x, np.float32)
+    w = np.ascontiguousarray(w, np.float32)
+    rc = np.ascontiguousarray(rc, np.float32)
+    assert x.size == HD and w.size == HD and rc.size == 64
+    out = np.zeros(HD, np.float32)
+    lib().kvo_qk_prep(_p(x), _p(w), _p(rc), _p(out))
+    return out

@@ -8,6 +8,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cmath>
 #include <cstdint>
 #include <cstdlib>
 #include <cstring>
@@ -113,6 +114,10 @@ struct Store {
     void * ml = nullptr;
     size_t ml_bytes = 0;
     int max_blocks = 0;
+    // RoPE table of the Q/K prep calls: [rope_rows][32] (cos, sin), the caller's or the store's own text table
+    const float2 * rope = nullptr;
+    int rope_rows = 0;
+    void * rope_own = nullptr;
     // mk_kv_profile: a pool of event sets recorded around each call's kernels on the launch stream; a set's elapsed times
     // are read only when the pool wraps around or profiling stops, so timed back-to-back calls never wait on the host
     struct EvSet {
@@ -139,6 +144,7 @@ struct Store {
         for (void * p : allocs) (void) hipFree(p);
         if (part) (void) hipFree(part);
         if (ml) (void) hipFree(ml);
+        if (rope_own) (void) hipFree(rope_own);
     }
     void grow(void *& p, size_t & have, size_t need) {
         if (need <= have) return;
@@ -273,6 +279,23 @@ int digest_seq(Store & s, int seq, unsigned long long * out, int cap) {
 
 } // namespace
 
+// the text RoPE table of the Q/K prep: row p, pair i = (cos, sin) of p * base^(-2i/64), base 1e7, computed in double
+// and rounded to float (loader.cu:1252-1258, mk_shared.cuh:240)
+static void use_default_rope(Store & s) {
+    if (!s.rope_own) {
+        std::vector<float2> t((size_t) s.ctx * 32);
+        for (int p = 0; p < s.ctx; p++)
+            for (int i = 0; i < 32; i++) {
+                const double th = (double) p * std::pow(10000000.0, -2.0 * i / 64.0);
+                t[(size_t) p * 32 + i] = make_float2((float) std::cos(th), (float) std::sin(th));
+            }
+        HCK(hipMalloc(&s.rope_own, t.size() * sizeof(float2)));
+        HCK(hipMemcpy(s.rope_own, t.data(), t.size() * sizeof(float2), hipMemcpyHostToDevice));
+    }
+    s.rope = static_cast<const float2 *>(s.rope_own);
+    s.rope_rows = s.ctx;
+}
+
 extern "C" {
 
 const char * mk_last_error(void) { return g_err.c_str(); }
@@ -373,7 +396,8 @@ int mk_kv_set_pages(void * h, int seq, const int * pages, int n) {
     });
 }
 
-int mk_kv_append(void * h, int seq, int layer0, int n_layers, int pos, int T, const void * k, const void * v, int dtype, void * stream) {
+static int append_impl(void * h, int seq, int layer0, int n_layers, int pos, int T, const void * k, const void * v, int dtype,
+                       const float * knw, void * stream) {
     return guarded([&] {
         Store & s = *as_store(h);
         check_seq(s, seq);
@@ -381,17 +405,23 @@ int mk_kv_append(void * h, int seq, int layer0, int n_layers, int pos, int T, co
         if (T < 1 || pos < 0 || pos + T > s.ctx) throw std::runtime_error("positions outside 0 .. ctx-1");
         if (dtype != 0 && dtype != 1) throw std::runtime_error("dtype: 0 fp32, 1 fp16");
         if (!k || !v) throw std::runtime_error("null K/V pointer");
+        if (knw) {
+            if (!s.rope) use_default_rope(s);
+            if (pos + T > s.rope_rows) throw std::runtime_error("positions beyond the RoPE table");
+        }
         Store::EvSet * es = prof_set(s, 2);
         HCK(launch_append(s.S, seq, layer0, n_layers, pos, T, k, v, dtype, static_cast<hipStream_t>(stream), es ? es->e[0] : nullptr,
-                          es ? es->e[1] : nullptr));
+                          es ? es->e[1] : nullptr, knw, knw ? s.rope : nullptr));
         s.top[seq] = std::max(s.top[seq], pos + T);
         s.n[seq] = std::max(s.n[seq], pos + T);
         return 0;
     });
 }
 
+// qs / gs: row strides (floats) of q and gate; qnw: q-norm weights (the Q prep) or null
 static int attend_impl(void * h, int layer0, int n_layers, int n_seq, const int * seqs, const int * lens, int T, const float * q,
-                       const float * gate, float * out, int8_t * q32a, int8_t * q32b, uint16_t * q32m, void * stream) {
+                       int qs, const float * qnw, const float * gate, int gs, float * out, int8_t * q32a, int8_t * q32b, uint16_t * q32m,
+                       void * stream) {
     return guarded([&] {
         Store & s = *as_store(h);
         if ((q32a != nullptr) != (q32b != nullptr) || (q32a != nullptr) != (q32m != nullptr))
@@ -405,6 +435,9 @@ static int attend_impl(void * h, int layer0, int n_layers, int n_seq, const int 
         a.S = s.S;
         a.T = T;
         a.gate = gate;
+        a.qs = qs;
+        a.gs = gs;
+        a.qnw = qnw;
         a.R = GQA * T;
         a.RP = a.R <= 8 ? 8 : 16; // one 8-row group (T = 1), else batches of 16 rows
         a.nseq = n_seq;
@@ -422,6 +455,12 @@ static int attend_impl(void * h, int layer0, int n_layers, int n_seq, const int 
             d.cs = seg_len(L);
             d.nseg = (L + d.cs - 1) / d.cs;
             seg_total += d.nseg;
+        }
+        if (qnw) {
+            if (!s.rope) use_default_rope(s);
+            for (int i = 0; i < n_seq; i++)
+                if (lens[i] > s.rope_rows) throw std::runtime_error("positions beyond the RoPE table");
+            a.rope = s.rope;
         }
         for (int l = 0; l < s.n_layers; l++) {
             a.krot |= (unsigned) s.spec.kr[l] << l;
@@ -447,9 +486,10 @@ static int attend_impl(void * h, int layer0, int n_layers, int n_seq, const int 
             }
             b.n_base = item;
             b.n_items = item * ((a.R + a.RP - 1) / a.RP);
-            b.q = q + (size_t) l * n_seq * T * NH * HD;
+            b.q = q + (size_t) l * n_seq * T * NH * qs;
             b.out = out + (size_t) l * n_seq * T * NH * HD;
-            if (gate) b.gate = gate + (size_t) l * n_seq * T * NH * HD;
+            if (gate) b.gate = gate + (size_t) l * n_seq * T * NH * gs;
+            if (qnw) b.qnw = qnw + (size_t) l * HD;
             if (q32a) {
                 b.q32a = q32a + (size_t) l * n_seq * T * 192 * 16;
                 b.q32b = q32b + (size_t) l * n_seq * T * 192 * 16;
@@ -473,19 +513,55 @@ static int attend_impl(void * h, int layer0, int n_layers, int n_seq, const int 
     });
 }
 
+int mk_kv_append(void * h, int seq, int layer0, int n_layers, int pos, int T, const void * k, const void * v, int dtype, void * stream) {
+    return append_impl(h, seq, layer0, n_layers, pos, T, k, v, dtype, nullptr, stream);
+}
+
+int mk_kv_append_prep(void * h, int seq, int layer0, int n_layers, int pos, int T, const float * k, const float * v, const float * k_norm,
+                      void * stream) {
+    if (!k_norm) {
+        g_err = "null k_norm pointer";
+        return -1;
+    }
+    return append_impl(h, seq, layer0, n_layers, pos, T, k, v, 0, k_norm, stream);
+}
+
 int mk_kv_attend(void * h, int layer0, int n_layers, int n_seq, const int * seqs, const int * lens, int T, const float * q, float * out,
                  void * stream) {
-    return attend_impl(h, layer0, n_layers, n_seq, seqs, lens, T, q, nullptr, out, nullptr, nullptr, nullptr, stream);
+    return attend_impl(h, layer0, n_layers, n_seq, seqs, lens, T, q, HD, nullptr, nullptr, HD, out, nullptr, nullptr, nullptr, stream);
 }
 
 int mk_kv_attend_gated(void * h, int layer0, int n_layers, int n_seq, const int * seqs, const int * lens, int T, const float * q,
                        const float * gate, float * out, void * q32a, void * q32b, unsigned short * q32meta, void * stream) {
+    if (!gate) {
+        g_err = "null gate pointer";
+        return -1;
+    }
+    return attend_impl(h, layer0, n_layers, n_seq, seqs, lens, T, q, HD, nullptr, gate, HD, out, static_cast<int8_t *>(q32a),
+                       static_cast<int8_t *>(q32b), q32meta, stream);
+}
+
+int mk_kv_attend_prep(void * h, int layer0, int n_layers, int n_seq, const int * seqs, const int * lens, int T, const float * qg,
+                      const float * q_norm, float * out, void * q32a, void * q32b, unsigned short * q32meta, void * stream) {
+    if (!qg || !q_norm) {
+        g_err = "null qg / q_norm pointer";
+        return -1;
+    }
+    return attend_impl(h, layer0, n_layers, n_seq, seqs, lens, T, qg, 2 * HD, q_norm, qg + HD, 2 * HD, out, static_cast<int8_t *>(q32a),
+                       static_cast<int8_t *>(q32b), q32meta, stream);
+}
+
+int mk_kv_set_rope(void * h, const void * table, int rows) {
     return guarded([&] {
-        if (!gate) throw std::runtime_error("null gate pointer");
-        const int r = attend_impl(h, layer0, n_layers, n_seq, seqs, lens, T, q, gate, out, static_cast<int8_t *>(q32a),
-                                  static_cast<int8_t *>(q32b), q32meta, stream);
-        if (r < 0) throw std::runtime_error(g_err); // (the message attend_impl left)
-        return r;
+        Store & s = *as_store(h);
+        if (!table) {
+            use_default_rope(s);
+            return 0;
+        }
+        if (rows < 1) throw std::runtime_error("RoPE table rows must be positive");
+        s.rope = static_cast<const float2 *>(table);
+        s.rope_rows = rows;
+        return 0;
     });
 }
 

@@ -524,8 +524,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NP == 1 ? 2
             half2v o0 = {(_Float16) 0.f, (_Float16) 0.f}, o1 = o0;
             if (row0 + r < a.R) {
                 const int hh = (row0 + r) / T, t = (row0 + r) % T;
-                const float4 x = *reinterpret_cast<const float4 *>(a.q + (((size_t) (l * a.nseq + si) * T + t) * NH + GQA * g + hh) * HD + 4 * lane);
+                const float4 x = *reinterpret_cast<const float4 *>(a.q + (((size_t) (l * a.nseq + si) * T + t) * NH + GQA * g + hh) * a.qs + 4 * lane);
                 float v[4] = {x.x, x.y, x.z, x.w};
+                if (a.qnw) qk_prep(v, a.qnw + (size_t) l * HD, a.rope + (size_t) (L - T + t) * 32);
                 if ((a.krot >> (a.layer0 + l)) & 1u) fwht256_w64(v);
                 o0[0] = (_Float16) (v[0] * 0.0625f);
                 o0[1] = (_Float16) (v[1] * 0.0625f);
@@ -712,7 +713,7 @@ __global__ __launch_bounds__(256) void k_combine(AttnArgs a) {
     const int h = GQA * g + r / T, t = r % T;
     const size_t trow = (size_t) (l * a.nseq + si) * T + t; // the token's row of 24 x 256 outputs
     if (a.gate) { // the sigmoid output gate (qwen38_mk.cu:4686)
-        const float4 gt = *reinterpret_cast<const float4 *>(a.gate + (trow * NH + h) * HD + 4 * lane);
+        const float4 gt = *reinterpret_cast<const float4 *>(a.gate + (trow * NH + h) * a.gs + 4 * lane);
         v[0] = v[0] / (1.0f + expf(-gt.x));
         v[1] = v[1] / (1.0f + expf(-gt.y));
         v[2] = v[2] / (1.0f + expf(-gt.z));

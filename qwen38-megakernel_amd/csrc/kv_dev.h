@@ -71,6 +71,35 @@ __device__ __forceinline__ void fwht256_w64(float (&v)[4]) {
     for (int k = 0; k < 4; k++) v[k] *= 0.0625f;
 }
 
+// Q/K prep of one row per wave (lane l holds values 4l .. 4l+3): RMSNorm over the 256 values with weight w and
+// eps 1e-6, then NeoX RoPE on values 0..63, pair (i, i + 32) rotated by the table row rc[i] = (cos, sin) of the
+// row's position (qwen38_mk.cu:2623-2636, 2903-2910, mk_shared.cuh:239).  The arithmetic order is fixed so that a
+// scalar restatement reproduces it bit for bit: per-lane sum of squares as an FMA chain, xor-butterfly over the
+// wave, 1 / sqrt (both correctly rounded), products and FMAs named explicitly.  All 64 lanes must call it.
+__device__ __forceinline__ void qk_prep(float (&v)[4], const float * w, const float2 * rc) {
+    const int lane = lane_id();
+    float s = __builtin_fmaf(v[3], v[3], __builtin_fmaf(v[2], v[2], __builtin_fmaf(v[1], v[1], v[0] * v[0])));
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) s = s + shfl_xor(s, m);
+    const float rs = 1.0f / __builtin_sqrtf(s / 256.0f + 1e-6f);
+    const float4 wv = *reinterpret_cast<const float4 *>(w + 4 * lane);
+    v[0] = v[0] * (rs * wv.x);
+    v[1] = v[1] * (rs * wv.y);
+    v[2] = v[2] * (rs * wv.z);
+    v[3] = v[3] * (rs * wv.w);
+    float o[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) o[k] = shfl_xor(v[k], 8);
+    if (lane < 16) {
+        const float4 * tab = reinterpret_cast<const float4 *>(rc + 4 * (lane & 7));
+        const float4 c01 = tab[0], c23 = tab[1];
+        const float c[4] = {c01.x, c01.z, c23.x, c23.z}, sn[4] = {c01.y, c01.w, c23.y, c23.w};
+#pragma unroll
+        for (int k = 0; k < 4; k++)
+            v[k] = lane < 8 ? __builtin_fmaf(v[k], c[k], -(o[k] * sn[k])) : __builtin_fmaf(o[k], sn[k], v[k] * c[k]);
+    }
+}
+
 // float -> int32 by the hardware conversion: truncates, saturates, NaN -> 0 (the reference's cvt.rzi; a C cast leaves
 // out-of-range and NaN undefined, so the instruction is named explicitly)
 __device__ __forceinline__ int f2i_rz(float x) {

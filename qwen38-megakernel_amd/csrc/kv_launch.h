@@ -28,7 +28,10 @@ struct AttnArgs {
     SeqDesc sd[8];
     const float * q;     // [nl][nseq][T][NH][HD] queries of this launch's layers (fp32, before the 1/16 scale)
     float * out;         // [nl][nseq][T][NH][HD]
-    const float * gate;  // optional [nl][nseq][T][NH][HD]: out = y / (1 + exp(-gate))
+    int qs, gs;          // row strides (floats) of q and gate: 256, or 512 for the q_proj layout [.. NH][q 256 | gate 256]
+    const float * qnw;   // optional [nl][HD] q-norm weights: q rows get RMSNorm + RoPE (qk_prep) before use
+    const float2 * rope; // with qnw: [positions][32] (cos, sin); row t of a sequence of length L is position L - T + t
+    const float * gate;  // optional [nl][nseq][T][NH][gs]: out = y / (1 + exp(-gate))
     int8_t * q32a;       // optional o_proj activation units of out: [nl][nseq][T][192][16] int8 (even blocks)
     int8_t * q32b;       // ... (odd blocks)
     uint16_t * q32m;     // ... [nl][nseq][T][192][4]: half scales of the a / b blocks, int sums of the a / b halves
@@ -50,8 +53,10 @@ constexpr int ATTN_LDS = AWAVES * STAGE_BYTES;   // one stage per wave (+ the qu
 
 // ev0 / ev1: optional events recorded at the kernel's own start and end (hipExtLaunchKernelGGL: the dispatch packet's
 // timestamps, the same the profiler reads), for the store's kernel timing
+// knw (optional): [nl][HD] k-norm weights; K rows then get RMSNorm + RoPE (qk_prep, table rope) before quantization
 hipError_t launch_append(const StoreLayout & S, int seq, int layer0, int nl, int pos, int T, const void * k, const void * v, int f16,
-                         hipStream_t st, hipEvent_t ev0 = nullptr, hipEvent_t ev1 = nullptr);
+                         hipStream_t st, hipEvent_t ev0 = nullptr, hipEvent_t ev1 = nullptr, const float * knw = nullptr,
+                         const float2 * rope = nullptr);
 hipError_t launch_ring_refill(const StoreLayout & S, int seq, int nl, int p0, int p1, hipStream_t st);
 hipError_t launch_attn(const AttnArgs & a, int kb, int vb, int max_blocks, hipStream_t st, hipEvent_t ev0 = nullptr,
                        hipEvent_t ev1 = nullptr);

@@ -1,6 +1,6 @@
 // Append/evict half of the KV path (gfx950, wave64).
 //
-// k_append      : new K/V rows -> optional 256-point FWHT -> main row in the side's format (q8 or 4..7-bit packed)
+// k_append      : new K/V rows -> optional K prep (RMSNorm + RoPE) -> optional 256-point FWHT -> main row in the side's format (q8 or 4..7-bit packed)
 //                 and, for sides with a window, the q8 ring copy of the same rotated values (kv_store,
 //                 qwen38_mk.cu:2099-2116).  Eviction from the window is ring-slot reuse plus the read-side window
 //                 rule: the packed row was written from the same fp32 values, so nothing is requantized later.
@@ -22,7 +22,7 @@ __device__ __forceinline__ size_t ring_row(const StoreLayout & S, int seq, int g
 
 // One wave per row; lane l holds values 4l .. 4l+3.  Rows of the input: [T][nl][NKV][256] (fp16 or fp32).
 __global__ __launch_bounds__(256) void k_append(StoreLayout S, int seq, int layer0, int nl, int pos, int T, const void * kin,
-                                                const void * vin, int f16) {
+                                                const void * vin, int f16, const float * knw, const float2 * rope) {
     const int wave = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (wave >= T * nl * NKV * 2) return;
     const int lane = threadIdx.x & 63;
@@ -49,8 +49,9 @@ __global__ __launch_bounds__(256) void k_append(StoreLayout S, int seq, int laye
         v[3] = raw.w;
     }
     const SideLayout & sd = S.side[layer0 + l][w];
-    if (sd.rot) fwht256_w64(v);
     const int p = pos + t;
+    if (knw && !w) qk_prep(v, knw + (size_t) l * HD, rope + (size_t) p * 32);
+    if (sd.rot) fwht256_w64(v);
     const size_t row = main_row(S, seq, g, p);
     uint16_t sc;
     if (sd.bits == 8) {
@@ -125,9 +126,10 @@ __global__ __launch_bounds__(256) void k_ring_refill(StoreLayout S, int seq, int
 }
 
 hipError_t launch_append(const StoreLayout & S, int seq, int layer0, int nl, int pos, int T, const void * k, const void * v, int f16,
-                         hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {
+                         hipStream_t st, hipEvent_t ev0, hipEvent_t ev1, const float * knw, const float2 * rope) {
     const int waves = T * nl * NKV * 2;
-    hipExtLaunchKernelGGL(k_append, dim3((waves + 3) / 4), dim3(256), 0, st, ev0, ev1, 0, S, seq, layer0, nl, pos, T, k, v, f16);
+    hipExtLaunchKernelGGL(k_append, dim3((waves + 3) / 4), dim3(256), 0, st, ev0, ev1, 0, S, seq, layer0, nl, pos, T, k, v, f16, knw,
+                          rope);
     return hipGetLastError();
 }
 

@@ -29,6 +29,10 @@ SIGNATURES = {
     "mk_kv_attend": (_c_int, [_c_vp, _c_int, _c_int, _c_int, _P_int, _P_int, _c_int, _c_vp, _c_vp, _c_vp]),
     "mk_kv_attend_gated": (_c_int, [_c_vp, _c_int, _c_int, _c_int, _P_int, _P_int, _c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _P_u16,
                                     _c_vp]),
+    "mk_kv_set_rope": (_c_int, [_c_vp, _c_vp, _c_int]),
+    "mk_kv_append_prep": (_c_int, [_c_vp, _c_int, _c_int, _c_int, _c_int, _c_int, _c_vp, _c_vp, _c_vp, _c_vp]),
+    "mk_kv_attend_prep": (_c_int, [_c_vp, _c_int, _c_int, _c_int, _P_int, _P_int, _c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _P_u16,
+                                   _c_vp]),
     "mk_truncate": (_c_int, [_c_vp, _c_int]),
     "mk_rewind_to": (_c_int, [_c_vp, _c_int]),
     "mk_kv_rewind": (_c_int, [_c_vp, _c_int, _c_int]),
@@ -149,6 +153,22 @@ class KVStore:
         l = (ctypes.c_int * n)(*lens)
         _check(lib().mk_kv_attend_gated(self.h, layer0, n_layers, n, s, l, T, q_ptr, gate_ptr, out_ptr, q32a or None, q32b or None,
                                         ctypes.cast(q32meta, _P_u16) if q32meta else None, stream))
+
+    def set_rope(self, table_ptr=0, rows=0):
+        """Use a device RoPE table [rows][32] (cos, sin) for the prep calls; 0 = the store's own text table."""
+        _check(lib().mk_kv_set_rope(self.h, table_ptr or None, rows))
+
+    def append_prep(self, seq, layer0, n_layers, pos, T, k_ptr, v_ptr, knorm_ptr, stream=0):
+        """append of raw fp32 K rows: RMSNorm (k_norm weights) + RoPE inside the append kernel."""
+        _check(lib().mk_kv_append_prep(self.h, seq, layer0, n_layers, pos, T, k_ptr, v_ptr, knorm_ptr, stream))
+
+    def attend_prep(self, layer0, n_layers, seqs, lens, T, qg_ptr, qnorm_ptr, out_ptr, q32a=0, q32b=0, q32meta=0, stream=0):
+        """attend_gated on the raw q_proj output [..][24][q 256 | gate 256]: q-norm + RoPE, attention, gate."""
+        n = len(seqs)
+        s = (ctypes.c_int * n)(*seqs)
+        l = (ctypes.c_int * n)(*lens)
+        _check(lib().mk_kv_attend_prep(self.h, layer0, n_layers, n, s, l, T, qg_ptr, qnorm_ptr, out_ptr, q32a or None, q32b or None,
+                                       ctypes.cast(q32meta, _P_u16) if q32meta else None, stream))
 
     def rewind(self, seq, pos):
         _check(lib().mk_kv_rewind(self.h, seq, pos))

@@ -76,5 +76,23 @@ def expected_attention(oracle, Q, Kl, Vl, T, krot, vrot, kbits, vbits, ws, kring
     return out
 
 
+def check_rows(oracle, st, K, V, seq=0, pos0=0, ring_from=0):
+    T, nl = K.shape[0], K.shape[1]
+    for l in range(nl):
+        for w, X in ((0, K), (1, V)):
+            bits = (st.vbits if w else st.kbits)[l]
+            rot = (st.vrot if w else st.krot)[l]
+            has_ring = st.win > 0 and bits != 8
+            for g in range(NKV):
+                mq, ms, rq, rs = oracle.store_rows(X[:, l, g], rot, bits, ring=True, threads=8)
+                q, s = st.read_rows(seq, l, w, g, pos0, T)
+                assert np.array_equal(q, mq), (l, w, g, "main values")
+                assert np.array_equal(s, ms), (l, w, g, "main scales")
+                if has_ring and ring_from < T:
+                    q, s = st.read_rows(seq, l, w, g, pos0 + ring_from, T - ring_from, ring=True)
+                    assert np.array_equal(q, rq[ring_from:]), (l, w, g, "ring values")
+                    assert np.array_equal(s, rs[ring_from:]), (l, w, g, "ring scales")
+
+
 def rel_err(got, ref):
     return float(np.abs(got.astype(np.float64) - ref).max() / max(np.abs(ref).max(), 1e-30))

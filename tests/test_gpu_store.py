@@ -3,29 +3,11 @@ and the state digest, bit for bit against the oracle."""
 import numpy as np
 import pytest
 
-from kvcase import HD, NKV, append_all, synth_kv
+from kvcase import HD, NKV, append_all, check_rows, synth_kv
 
 pytestmark = pytest.mark.gpu
 
 SPECS = ["", "K*=5r,V*=6", "K*=5r,V*=5", "K*=4,V*=7r", "*=6r", "K0=8,V0=5r,K1=7,V1=4"]
-
-
-def check_rows(oracle, st, K, V, seq=0, pos0=0, ring_from=0):
-    T, nl = K.shape[0], K.shape[1]
-    for l in range(nl):
-        for w, X in ((0, K), (1, V)):
-            bits = (st.vbits if w else st.kbits)[l]
-            rot = (st.vrot if w else st.krot)[l]
-            has_ring = st.win > 0 and bits != 8
-            for g in range(NKV):
-                mq, ms, rq, rs = oracle.store_rows(X[:, l, g], rot, bits, ring=True, threads=8)
-                q, s = st.read_rows(seq, l, w, g, pos0, T)
-                assert np.array_equal(q, mq), (l, w, g, "main values")
-                assert np.array_equal(s, ms), (l, w, g, "main scales")
-                if has_ring and ring_from < T:
-                    q, s = st.read_rows(seq, l, w, g, pos0 + ring_from, T - ring_from, ring=True)
-                    assert np.array_equal(q, rq[ring_from:]), (l, w, g, "ring values")
-                    assert np.array_equal(s, rs[ring_from:]), (l, w, g, "ring scales")
 
 
 @pytest.mark.parametrize("spec", SPECS)

@@ -103,6 +103,29 @@ int mk_kv_append_prep(void * h, int seq, int layer0, int n_layers, int pos, int 
 int mk_kv_attend_prep(void * h, int layer0, int n_layers, int n_seq, const int * seqs, const int * lens, int T, const float * qg,
                       const float * q_norm, float * out, void * q32a, void * q32b, unsigned short * q32meta, void * stream);
 
+/*
+ * Prefill of positions pos .. pos+T-1 of sequence seq (pos = the stored length, no gap) for slots layer0 ..
+ * layer0+n_layers-1: stores the K/V rows (k, v [T][n_layers][4][256], dtype as mk_kv_append) and computes the causal
+ * attention of the chunk's queries (q [n_layers][T][24][256], after RMSNorm/RoPE) over the store, out of the same
+ * shape.  The chunk runs in pieces ending at 640-position bucket boundaries, each piece stored and then attended, so
+ * its rows read the window of their bucket from the ring (MK_EXACT prefill, prefill_host.cu:606-615).  Each output
+ * is a function of its position and the stored rows only: the result does not depend on how a prompt is split into
+ * chunks (pk_attn8's exact form, prefill_attn.cuh:698-702).  Replaces pk_attn_prep's kv_store + attn (pk_attn8 /
+ * pk_attn9 + combine) of mk_prefill.  Asynchronous on `stream`.
+ */
+int mk_kv_prefill(void * h, int seq, int layer0, int n_layers, int pos, int T, const void * k, const void * v, int dtype, const float * q,
+                  float * out, void * stream);
+
+/*
+ * mk_kv_prefill on the raw projections with the whole attention block of a prefill layer: K before the k-norm / RoPE
+ * (fp32), qg [n_layers][T][24][512] (query 256 | gate 256 per head), k_norm / q_norm [n_layers][256]; out gated, and
+ * the optional q32 set [n_layers][T][192][16 | 4] as mk_kv_attend_gated (pk_attn_prep, attention, pk_attn_out:
+ * prefill.cuh:986-1060).
+ */
+int mk_kv_prefill_prep(void * h, int seq, int layer0, int n_layers, int pos, int T, const float * k, const float * v, const float * k_norm,
+                       const float * qg, const float * q_norm, float * out, void * q32a, void * q32b, unsigned short * q32meta,
+                       void * stream);
+
 /* Rewind sequence 0 / sequence seq to position pos: ring rows refilled from the main store (ring_rewind,
  * ck_pool.cu:285-296; k_ring_refill, qwen38_mk.cu:2485-2517).  mk_truncate / mk_rewind_to replace capi.cpp:572 / 601. */
 int mk_truncate(void * h, int len);

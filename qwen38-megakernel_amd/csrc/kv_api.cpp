@@ -551,6 +551,91 @@ int mk_kv_attend_prep(void * h, int layer0, int n_layers, int n_seq, const int *
                        static_cast<int8_t *>(q32b), q32meta, stream);
 }
 
+// prefill: the chunk pos .. pos+T-1 in pieces ending at 640-bucket boundaries; each piece's K/V rows are stored, then
+// every layer's queries of the piece attend (prefill_host.cu:606-615).  k, v: [T][n_layers][4][256]; q: [n_layers][T][24][qs];
+// out: [n_layers][T][24][256]; gate [n_layers][T][24][gs]; q32 [n_layers][T][192][16 | 4].
+static int prefill_impl(void * h, int seq, int layer0, int n_layers, int pos, int T, const void * k, const void * v, int dtype,
+                        const float * knw, const float * q, int qs, const float * qnw, const float * gate, int gs, float * out,
+                        int8_t * q32a, int8_t * q32b, uint16_t * q32m, void * stream) {
+    return guarded([&] {
+        Store & s = *as_store(h);
+        check_seq(s, seq);
+        check_layers(s, layer0, n_layers);
+        if (T < 1 || pos < 0 || pos + T > s.ctx) throw std::runtime_error("positions outside 0 .. ctx-1");
+        if (pos > s.n[seq]) throw std::runtime_error("prefill from position " + std::to_string(pos) + " leaves a gap after the " +
+                                                     std::to_string(s.n[seq]) + " stored positions");
+        if (dtype != 0 && dtype != 1) throw std::runtime_error("dtype: 0 fp32, 1 fp16");
+        if (!k || !v || !q || !out) throw std::runtime_error("null k/v/q/out pointer");
+        if ((q32a != nullptr) != (q32b != nullptr) || (q32a != nullptr) != (q32m != nullptr))
+            throw std::runtime_error("the q32 outputs come as a set: a, b and meta");
+        if (knw || qnw) {
+            if (!s.rope) use_default_rope(s);
+            if (pos + T > s.rope_rows) throw std::runtime_error("positions beyond the RoPE table");
+        }
+        hipStream_t st = static_cast<hipStream_t>(stream);
+        const size_t esz = dtype ? 2 : 4, krow = (size_t) n_layers * NKV * HD;
+        for (int a0 = 0; a0 < T;) {
+            const int b = std::min(T, ((pos + a0) / ATT_BUCKET_ + 1) * ATT_BUCKET_ - pos);
+            const int n0 = pos + a0, Tp = b - a0;
+            HCK(launch_append(s.S, seq, layer0, n_layers, n0, Tp, static_cast<const char *>(k) + a0 * krow * esz,
+                              static_cast<const char *>(v) + a0 * krow * esz, dtype, st, nullptr, nullptr, knw, knw ? s.rope : nullptr));
+            s.top[seq] = std::max(s.top[seq], n0 + Tp);
+            s.n[seq] = std::max(s.n[seq], n0 + Tp);
+            PrefillArgs p{};
+            p.S = s.S;
+            p.seq = seq;
+            p.n0 = n0;
+            p.Tp = Tp;
+            p.L = n0 + Tp;
+            p.ws = window_start(p.L, s.win);
+            p.R = GQA * Tp;
+            p.nrb = (p.R + PF_ROWS - 1) / PF_ROWS;
+            p.nseg = (p.L + PF_SEG - 1) / PF_SEG;
+            p.qs = qs;
+            p.gs = gs;
+            p.rope = qnw ? s.rope : nullptr;
+            s.grow(s.part, s.part_bytes, (size_t) NKV * p.nseg * p.R * HD * sizeof(float));
+            s.grow(s.ml, s.ml_bytes, (size_t) NKV * p.nseg * p.R * sizeof(float2));
+            p.part = static_cast<float *>(s.part);
+            p.ml = static_cast<float2 *>(s.ml);
+            for (int l = 0; l < n_layers; l++) {
+                const int sl = layer0 + l;
+                const size_t trow = (size_t) l * T + a0; // first token row of the piece in this layer's block
+                p.layer = sl;
+                p.krot = s.spec.kr[sl];
+                p.vrot = s.spec.vr[sl];
+                p.q = q + trow * NH * qs;
+                p.qnw = qnw ? qnw + (size_t) l * HD : nullptr;
+                p.out = out + trow * NH * HD;
+                p.gate = gate ? gate + trow * NH * gs : nullptr;
+                p.q32a = q32a ? q32a + trow * 192 * 16 : nullptr;
+                p.q32b = q32b ? q32b + trow * 192 * 16 : nullptr;
+                p.q32m = q32m ? q32m + trow * 192 * 4 : nullptr;
+                HCK(launch_prefill(p, s.S.side[sl][0].bits, s.S.side[sl][1].bits, st));
+            }
+            a0 = b;
+        }
+        return 0;
+    });
+}
+
+int mk_kv_prefill(void * h, int seq, int layer0, int n_layers, int pos, int T, const void * k, const void * v, int dtype, const float * q,
+                  float * out, void * stream) {
+    return prefill_impl(h, seq, layer0, n_layers, pos, T, k, v, dtype, nullptr, q, HD, nullptr, nullptr, HD, out, nullptr, nullptr, nullptr,
+                        stream);
+}
+
+int mk_kv_prefill_prep(void * h, int seq, int layer0, int n_layers, int pos, int T, const float * k, const float * v, const float * k_norm,
+                       const float * qg, const float * q_norm, float * out, void * q32a, void * q32b, unsigned short * q32meta,
+                       void * stream) {
+    if (!k_norm || !qg || !q_norm) {
+        g_err = "null k_norm / qg / q_norm pointer";
+        return -1;
+    }
+    return prefill_impl(h, seq, layer0, n_layers, pos, T, k, v, 0, k_norm, qg, 2 * HD, q_norm, qg + HD, 2 * HD, out,
+                        static_cast<int8_t *>(q32a), static_cast<int8_t *>(q32b), q32meta, stream);
+}
+
 int mk_kv_set_rope(void * h, const void * table, int rows) {
     return guarded([&] {
         Store & s = *as_store(h);

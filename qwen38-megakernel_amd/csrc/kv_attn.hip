@@ -637,6 +637,47 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NP == 1 ? 2
     }
 }
 
+// ------------------------------------------------------------------------------------------------ output epilogue
+// One output row y (head h of token row trow, lane l holding dims 4l .. 4l+3) after the merge: the V un-rotation when
+// V is stored rotated, the sigmoid output gate (qwen38_mk.cu:4686) when grow is given, the fp32 store, and when q32a
+// is given the o_proj activation units of q32_store (qwen38_mk.cu:283-307): block k = lane / 8 of the head's 8 blocks of
+// 32 (j = 8 h + k), amax / 127, round half away from zero; unit gi = 8 h + 2 (k / 2) + half, bytes of the even blocks
+// in a, odd ones in b.  All 64 lanes of the wave call it.
+__device__ __forceinline__ void finish_row(float (&v)[4], bool vrot, const float * grow, float * orow, int8_t * q32a, int8_t * q32b,
+                                           uint16_t * q32m, size_t trow, int h) {
+    const int lane = lane_id();
+    if (vrot) fwht256_w64(v);
+    if (grow) {
+        const float4 gt = *reinterpret_cast<const float4 *>(grow + 4 * lane);
+        v[0] = v[0] / (1.0f + expf(-gt.x));
+        v[1] = v[1] / (1.0f + expf(-gt.y));
+        v[2] = v[2] / (1.0f + expf(-gt.z));
+        v[3] = v[3] / (1.0f + expf(-gt.w));
+    }
+    *reinterpret_cast<float4 *>(orow + 4 * lane) = make_float4(v[0], v[1], v[2], v[3]);
+    if (q32a) {
+        float am = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+        am = fmaxf(am, shfl_xor(am, 1));
+        am = fmaxf(am, shfl_xor(am, 2));
+        am = fmaxf(am, shfl_xor(am, 4));
+        const float d = am / 127.0f;
+        int qv[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) qv[k] = am == 0.0f ? 0 : (int) roundf(v[k] / d);
+        const int k8 = lane >> 3, part = k8 & 1, hh = (lane >> 2) & 1;
+        const size_t gi = trow * 192 + 8 * h + 2 * (k8 >> 1) + hh;
+        const unsigned packed = (qv[0] & 0xff) | (qv[1] & 0xff) << 8 | (qv[2] & 0xff) << 16 | (unsigned) (qv[3] & 0xff) << 24;
+        *reinterpret_cast<unsigned *>((part ? q32b : q32a) + gi * 16 + 4 * (lane & 3)) = packed;
+        int sum = qv[0] + qv[1] + qv[2] + qv[3];
+        sum += __shfl_xor(sum, 1, 64);
+        sum += __shfl_xor(sum, 2, 64);
+        if ((lane & 3) == 0) {
+            q32m[gi * 4 + part] = f2h_bits(d);
+            q32m[gi * 4 + 2 + part] = (uint16_t) (int16_t) sum;
+        }
+    }
+}
+
 // ------------------------------------------------------------------------------------------------ combine
 // One workgroup per output row (layer, sequence, kv head, row r): the merge of the head's segment partials
 // (attn_combine, qwen38_mk.cu:4617-4700: y = sum_c e_c O_c / sum_c e_c l_c with e_c = exp(m_c - M)).  Wave w loads the
@@ -709,40 +750,10 @@ __global__ __launch_bounds__(256) void k_combine(AttnArgs a) {
         dd = __builtin_fmaf(e, md.y, dd);
     }
     float v[4] = {y.x / dd, y.y / dd, y.z / dd, y.w / dd};
-    if ((a.vrot >> (a.layer0 + l)) & 1u) fwht256_w64(v);
     const int h = GQA * g + r / T, t = r % T;
     const size_t trow = (size_t) (l * a.nseq + si) * T + t; // the token's row of 24 x 256 outputs
-    if (a.gate) { // the sigmoid output gate (qwen38_mk.cu:4686)
-        const float4 gt = *reinterpret_cast<const float4 *>(a.gate + (trow * NH + h) * a.gs + 4 * lane);
-        v[0] = v[0] / (1.0f + expf(-gt.x));
-        v[1] = v[1] / (1.0f + expf(-gt.y));
-        v[2] = v[2] / (1.0f + expf(-gt.z));
-        v[3] = v[3] / (1.0f + expf(-gt.w));
-    }
-    *reinterpret_cast<float4 *>(a.out + (trow * NH + h) * HD + 4 * lane) = make_float4(v[0], v[1], v[2], v[3]);
-    if (a.q32a) {
-        // q32_store (qwen38_mk.cu:283-307): block k = lane / 8 of the head's 8 blocks of 32 (j = 8 h + k), amax / 127,
-        // round half away from zero; unit gi = 8 h + 2 (k / 2) + half, bytes of the even blocks in a, odd ones in b
-        float am = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-        am = fmaxf(am, shfl_xor(am, 1));
-        am = fmaxf(am, shfl_xor(am, 2));
-        am = fmaxf(am, shfl_xor(am, 4));
-        const float d = am / 127.0f;
-        int qv[4];
-#pragma unroll
-        for (int k = 0; k < 4; k++) qv[k] = am == 0.0f ? 0 : (int) roundf(v[k] / d);
-        const int k8 = lane >> 3, part = k8 & 1, hh = (lane >> 2) & 1;
-        const size_t gi = trow * 192 + 8 * h + 2 * (k8 >> 1) + hh;
-        const unsigned packed = (qv[0] & 0xff) | (qv[1] & 0xff) << 8 | (qv[2] & 0xff) << 16 | (unsigned) (qv[3] & 0xff) << 24;
-        *reinterpret_cast<unsigned *>((part ? a.q32b : a.q32a) + gi * 16 + 4 * (lane & 3)) = packed;
-        int sum = qv[0] + qv[1] + qv[2] + qv[3];
-        sum += __shfl_xor(sum, 1, 64);
-        sum += __shfl_xor(sum, 2, 64);
-        if ((lane & 3) == 0) {
-            a.q32m[gi * 4 + part] = f2h_bits(d);
-            a.q32m[gi * 4 + 2 + part] = (uint16_t) (int16_t) sum;
-        }
-    }
+    finish_row(v, (a.vrot >> (a.layer0 + l)) & 1u, a.gate ? a.gate + (trow * NH + h) * a.gs : nullptr, a.out + (trow * NH + h) * HD,
+               a.q32a, a.q32b, a.q32m, trow, h);
 }
 
 // The same merge for launches without rotated V, spread wider: one workgroup per (output row, 64-dim quarter).  Lane
@@ -835,6 +846,167 @@ hipError_t launch_combine(const AttnArgs & a, hipStream_t st, hipEvent_t ev0, hi
     return hipGetLastError();
 }
 
+// ------------------------------------------------------------------------------------------------ prefill
+// Causal attention of one prefill piece (pk_attn8's exact form, prefill_attn.cuh:698-702; pieces and window
+// prefill_host.cu:606-615).  Workgroup = (64 query rows, kv head, key segment k of PF_SEG positions), row block
+// fastest so the workgroups of one segment run side by side.  Tiles are staged once per workgroup (PF_NS stages,
+// tile i copied by wave i % 4, two tiles in flight) and every wave runs compute_tile for its 16 rows on the shared
+// stage.  A row's partial for segment k is one online softmax over the segment's tiles in order, and the combine folds
+// a row's segments 0 .. pos / PF_SEG in order: each output is a function of its position and the store only, whatever
+// the chunking of the prefill.
+template <int KB, int VB>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void k_prefill(PrefillArgs a) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63, n = lane & 15, q = lane >> 4;
+    const StoreLayout & S = a.S;
+    int b = blockIdx.x;
+    const int rb = b % a.nrb;
+    b /= a.nrb;
+    const int g = b % NKV, k = b / NKV;
+    const int r0 = PF_ROWS * rb, rlast = min(a.R, r0 + PF_ROWS) - 1;
+    const int pmax = a.n0 + rlast / GQA; // the last position any row of the block sees
+    const int c0 = k * PF_SEG;
+    if (c0 > pmax) return; // (no row of the block reads this segment: the combine skips it too)
+    const int c1 = min(c0 + PF_SEG, pmax + 1);
+    const int ntiles = (c1 - c0 + ATP - 1) / ATP;
+    const unsigned lds0 = (unsigned) (size_t) (__attribute__((address_space(3))) uint8_t *) smem;
+    half8 * const sQ = reinterpret_cast<half8 *>(smem + PF_NS * STAGE_BYTES); // [64][256] fp16, chunk-swizzled
+    const SideLayout & SK = S.side[a.layer][0];
+    const SideLayout & SV = S.side[a.layer][1];
+    const size_t ring0 = (size_t) (a.seq * NKV + g) * S.kvrc;
+    const int L = a.L, ws = a.ws;
+
+    auto issue = [&](int i) {
+        const int p0 = c0 + ATP * i, nv = min(ATP, L - p0);
+        const unsigned lds = (unsigned) __builtin_amdgcn_readfirstlane(lds0 + (i % PF_NS) * STAGE_BYTES);
+        const bool ring = S.kvrc > 0 && p0 >= ws;
+        TileSrc t;
+        size_t mr = 0;
+        if (!ring || !SK.ring || !SV.ring) mr = attn_main_row(S, a.seq, g, p0);
+        const size_t rr = ring ? ring0 + __builtin_amdgcn_readfirstlane(p0 % max(S.kvrc, 1)) : 0;
+        if (ring && SK.ring) {
+            t.k = reinterpret_cast<const uint8_t *>(SK.ring) + rr * HD;
+            t.ks = SK.rsc + rr * 8;
+        } else {
+            t.k = SK.vals + mr * (ring ? HD : 32 * KB);
+            t.ks = SK.scs + mr * 8;
+        }
+        if (ring && SV.ring) {
+            t.v = reinterpret_cast<const uint8_t *>(SV.ring) + rr * HD;
+            t.vs = SV.rsc + rr * 8;
+        } else {
+            t.v = SV.vals + mr * (ring ? HD : 32 * VB);
+            t.vs = SV.scs + mr * 8;
+        }
+        if (ring) issue_tile<8, 8>(t, nv, lds, lane);
+        else issue_tile<KB, VB>(t, nv, lds, lane);
+    };
+    // the first two tiles stream in while the query rows are prepared
+    if (wv == 0 && ntiles > 0) issue(0);
+    if (wv == 1 && ntiles > 1) issue(1);
+    const bool krot = a.krot;
+    for (int j = 0; j < 16; j++) {
+        const int rl = 16 * wv + j, r = r0 + rl;
+        half2v o0 = {(_Float16) 0.f, (_Float16) 0.f}, o1 = o0;
+        if (r < a.R) {
+            const int t = r / GQA, hh = r - GQA * t;
+            const float4 x = *reinterpret_cast<const float4 *>(a.q + ((size_t) t * NH + GQA * g + hh) * a.qs + 4 * lane);
+            float v[4] = {x.x, x.y, x.z, x.w};
+            if (a.qnw) qk_prep(v, a.qnw, a.rope + (size_t) (a.n0 + t) * 32);
+            if (krot) fwht256_w64(v);
+            o0[0] = (_Float16) (v[0] * 0.0625f);
+            o0[1] = (_Float16) (v[1] * 0.0625f);
+            o1[0] = (_Float16) (v[2] * 0.0625f);
+            o1[1] = (_Float16) (v[3] * 0.0625f);
+        }
+        reinterpret_cast<uint2 *>(sQ + qchunk(rl, lane >> 1))[lane & 1] = make_uint2(as_u(o0), as_u(o1));
+    }
+    WaveState<2> st;
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        st.m[h] = -INFINITY;
+        st.l[h] = 0.f;
+        const int r = r0 + 16 * wv + 8 * h + (n >> 1);
+        st.lim[h] = r < a.R ? a.n0 + r / GQA : -1;
+#pragma unroll
+        for (int bb = 0; bb < 8; bb++) st.acc[h][bb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    st.lim_min = a.n0 + (r0 + 16 * wv) / GQA; // (padding rows: zero queries, their scores are never read)
+    const half8 * const sQw = sQ + 16 * wv * (HD / 8);
+    for (int i = 0; i < ntiles; i++) {
+        if (wv == i % 4) vm_wait<0>(); // the copies of tile i have landed (the wave's only ones in flight)
+        __syncthreads();               // tile i visible to every wave; every wave is done with tile i - 1's stage
+        if (i + 2 < ntiles && wv == (i + 2) % 4) issue(i + 2);
+        const uint8_t * const stp = smem + (i % PF_NS) * STAGE_BYTES;
+        const int p0 = c0 + ATP * i;
+        if (S.kvrc > 0 && p0 >= ws) {
+            RawTile<8, 8> raw;
+            read_k<8, 8>(raw, stp, n, q);
+            read_v<8, 8>(raw, stp, n, q);
+            lds_drain();
+            compute_tile<2, 8, 8>(st, sQw, p0, raw);
+        } else {
+            RawTile<KB, VB> raw;
+            read_k<KB, VB>(raw, stp, n, q);
+            read_v<KB, VB>(raw, stp, n, q);
+            lds_drain();
+            compute_tile<2, KB, VB>(st, sQw, p0, raw);
+        }
+    }
+    // ---- the wave's 16 partial rows: O through an LDS buffer of its own (coalesced rows), (m, l) per row
+    constexpr int OLD = HD + 4;
+    static_assert(AWAVES * 16 * OLD * 4 <= PF_NS * STAGE_BYTES + PF_ROWS * HD * 2, "prefill row buffers");
+    __syncthreads(); // every wave is done with the stages and the query rows
+    float * const ob = reinterpret_cast<float *>(smem) + wv * 16 * OLD;
+    const size_t unit = (size_t) (g * a.nseg + k) * a.R;
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        float * o = ob + (8 * h + (n >> 1)) * OLD + 64 * q + (n & 1);
+#pragma unroll
+        for (int bb = 0; bb < 8; bb++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) o[16 * i + 2 * bb] = st.acc[h][bb][i];
+        const int r = r0 + 16 * wv + 8 * h + (n >> 1);
+        if (q == 0 && !(n & 1) && r < a.R) a.ml[unit + r] = make_float2(st.m[h], st.l[h]);
+    }
+    __syncthreads();
+    for (int j = 0; j < 16; j++) {
+        const int r = r0 + 16 * wv + j;
+        if (r < a.R)
+            *reinterpret_cast<float4 *>(a.part + (unit + r) * HD + 4 * lane) = *reinterpret_cast<const float4 *>(ob + j * OLD + 4 * lane);
+    }
+}
+
+// One wave per (row, kv head) of a prefill piece: the row's segments 0 .. pos / PF_SEG folded in segment order
+// (M' = max(M, m_k), O' = O e^(M - M') + O_k e^(m_k - M'), l likewise), y = O / l, then the output epilogue.
+__global__ __launch_bounds__(256) void k_prefill_combine(PrefillArgs a) {
+    const int wid = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (wid >= a.R * NKV) return;
+    const int r = wid % a.R, g = wid / a.R;
+    const int t = r / GQA, hh = r - GQA * t, pos = a.n0 + t;
+    const int nk = pos / PF_SEG + 1;
+    float M = -INFINITY, den = 0.f;
+    float4 num = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int k = 0; k < nk; k++) {
+        const size_t u = (size_t) (g * a.nseg + k) * a.R + r;
+        const float2 ml = a.ml[u];
+        const float4 o = *reinterpret_cast<const float4 *>(a.part + u * HD + 4 * lane);
+        const float Mn = fmaxf(M, ml.x);
+        const float e0 = M == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(M - Mn);
+        const float e1 = ml.x == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ml.x - Mn);
+        num.x = __builtin_fmaf(num.x, e0, e1 * o.x);
+        num.y = __builtin_fmaf(num.y, e0, e1 * o.y);
+        num.z = __builtin_fmaf(num.z, e0, e1 * o.z);
+        num.w = __builtin_fmaf(num.w, e0, e1 * o.w);
+        den = __builtin_fmaf(den, e0, e1 * ml.y);
+        M = Mn;
+    }
+    float v[4] = {num.x / den, num.y / den, num.z / den, num.w / den};
+    const int h = GQA * g + hh;
+    finish_row(v, a.vrot, a.gate ? a.gate + ((size_t) t * NH + h) * a.gs : nullptr, a.out + ((size_t) t * NH + h) * HD, a.q32a,
+               a.q32b, a.q32m, (size_t) t, h);
+}
+
 // ------------------------------------------------------------------------------------------------ dispatch
 typedef void (*AttnKernel)(AttnArgs);
 
@@ -879,6 +1051,49 @@ hipError_t launch_attn(const AttnArgs & a, int kb, int vb, int max_blocks, hipSt
     int blocks = a.n_items;
     if (max_blocks > 0 && blocks > max_blocks) blocks = max_blocks;
     hipExtLaunchKernelGGL(k, dim3(blocks), dim3(256), lds, st, ev0, ev1, 0, a);
+    return hipGetLastError();
+}
+
+typedef void (*PrefillKernel)(PrefillArgs);
+
+static PrefillKernel pick_prefill(int kb, int vb) {
+#define QKV_VB(K)                                                                                                      \
+    switch (vb) {                                                                                                      \
+    case 4: return k_prefill<K, 4>;                                                                                    \
+    case 5: return k_prefill<K, 5>;                                                                                    \
+    case 6: return k_prefill<K, 6>;                                                                                    \
+    case 7: return k_prefill<K, 7>;                                                                                    \
+    case 8: return k_prefill<K, 8>;                                                                                    \
+    default: return nullptr;                                                                                           \
+    }
+    switch (kb) {
+    case 4: QKV_VB(4)
+    case 5: QKV_VB(5)
+    case 6: QKV_VB(6)
+    case 7: QKV_VB(7)
+    case 8: QKV_VB(8)
+    default: return nullptr;
+    }
+#undef QKV_VB
+}
+
+hipError_t launch_prefill(const PrefillArgs & a, int kb, int vb, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {
+    PrefillKernel k = pick_prefill(kb, vb);
+    if (!k) return hipErrorInvalidValue;
+    constexpr int lds = PF_NS * STAGE_BYTES + PF_ROWS * HD * 2;
+    static thread_local const void * configured[32];
+    static thread_local int n_configured = 0;
+    bool done = false;
+    for (int i = 0; i < n_configured; i++) done |= configured[i] == (const void *) k;
+    if (!done) {
+        const hipError_t e = hipFuncSetAttribute((const void *) k, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+        if (e != hipSuccess) return e;
+        if (n_configured < 32) configured[n_configured++] = (const void *) k;
+    }
+    hipExtLaunchKernelGGL(k, dim3(a.nrb * NKV * a.nseg), dim3(256), lds, st, ev0, nullptr, 0, a);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipExtLaunchKernelGGL(k_prefill_combine, dim3((a.R * NKV + 3) / 4), dim3(256), 0, st, nullptr, ev1, 0, a);
     return hipGetLastError();
 }
 

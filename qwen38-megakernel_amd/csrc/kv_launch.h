@@ -39,6 +39,31 @@ struct AttnArgs {
     float2 * ml;         // [item][R] per-segment (max in log2 units, sum)
 };
 
+// one prefill piece of one layer: query rows r = 6 t + hh (token t = 0 .. Tp-1 at position n0 + t, query head
+// 6 g + hh of kv head g), keys in absolute segments of PF_SEG positions
+struct PrefillArgs {
+    StoreLayout S;
+    int layer, seq;
+    int n0, Tp, L, ws; // first query position, rows' tokens, L = n0 + Tp (one 640-bucket), window start of the bucket
+    int R, nrb, nseg;  // 6 Tp rows per kv head, ceil(R / PF_ROWS) row blocks, ceil(L / PF_SEG) key segments
+    int krot, vrot;
+    const float * q;   // [Tp][NH][qs]
+    int qs;
+    const float * qnw; // optional q-norm weights [HD] (the Q prep, table rope)
+    const float2 * rope;
+    float * out;       // [Tp][NH][HD]
+    const float * gate; // optional [Tp][NH][gs]
+    int gs;
+    int8_t * q32a;     // optional o_proj units [Tp][192][16] (a / b), meta [Tp][192][4]
+    int8_t * q32b;
+    uint16_t * q32m;
+    float * part;      // [NKV][nseg][R][HD] per-segment partial outputs (unnormalised)
+    float2 * ml;       // [NKV][nseg][R] (max in log2 units, sum)
+};
+constexpr int PF_SEG = 8192; // key positions per prefill segment (a multiple of 32)
+constexpr int PF_ROWS = 64;  // query rows per prefill workgroup (16 per wave)
+constexpr int PF_NS = 3;     // tile stages of a prefill workgroup (two tiles in flight)
+
 // canonical segment length: 32 * max(4, ceil(Lb / 4096)) with Lb = L rounded up to a 640 bucket, so at most 128
 // segments per kv head (one layer's 4 heads fill 2 workgroups on each of the 256 CUs) and the same partition for every
 // row count T whose rows share one bucket
@@ -61,5 +86,6 @@ hipError_t launch_ring_refill(const StoreLayout & S, int seq, int nl, int p0, in
 hipError_t launch_attn(const AttnArgs & a, int kb, int vb, int max_blocks, hipStream_t st, hipEvent_t ev0 = nullptr,
                        hipEvent_t ev1 = nullptr);
 hipError_t launch_combine(const AttnArgs & a, hipStream_t st, hipEvent_t ev0 = nullptr, hipEvent_t ev1 = nullptr);
+hipError_t launch_prefill(const PrefillArgs & a, int kb, int vb, hipStream_t st, hipEvent_t ev0 = nullptr, hipEvent_t ev1 = nullptr);
 
 } // namespace qkv

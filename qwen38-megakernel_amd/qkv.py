@@ -33,6 +33,9 @@ SIGNATURES = {
     "mk_kv_append_prep": (_c_int, [_c_vp, _c_int, _c_int, _c_int, _c_int, _c_int, _c_vp, _c_vp, _c_vp, _c_vp]),
     "mk_kv_attend_prep": (_c_int, [_c_vp, _c_int, _c_int, _c_int, _P_int, _P_int, _c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _P_u16,
                                    _c_vp]),
+    "mk_kv_prefill": (_c_int, [_c_vp, _c_int, _c_int, _c_int, _c_int, _c_int, _c_vp, _c_vp, _c_int, _c_vp, _c_vp, _c_vp]),
+    "mk_kv_prefill_prep": (_c_int, [_c_vp, _c_int, _c_int, _c_int, _c_int, _c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,
+                                    _P_u16, _c_vp]),
     "mk_truncate": (_c_int, [_c_vp, _c_int]),
     "mk_rewind_to": (_c_int, [_c_vp, _c_int]),
     "mk_kv_rewind": (_c_int, [_c_vp, _c_int, _c_int]),
@@ -169,6 +172,16 @@ class KVStore:
         l = (ctypes.c_int * n)(*lens)
         _check(lib().mk_kv_attend_prep(self.h, layer0, n_layers, n, s, l, T, qg_ptr, qnorm_ptr, out_ptr, q32a or None, q32b or None,
                                        ctypes.cast(q32meta, _P_u16) if q32meta else None, stream))
+
+    def prefill(self, seq, layer0, n_layers, pos, T, k_ptr, v_ptr, dtype, q_ptr, out_ptr, stream=0):
+        """Store K/V of positions pos .. pos+T-1 and attend the chunk's queries causally (640-bucket pieces)."""
+        _check(lib().mk_kv_prefill(self.h, seq, layer0, n_layers, pos, T, k_ptr, v_ptr, dtype, q_ptr, out_ptr, stream))
+
+    def prefill_prep(self, seq, layer0, n_layers, pos, T, k_ptr, v_ptr, knorm_ptr, qg_ptr, qnorm_ptr, out_ptr, q32a=0, q32b=0, q32meta=0,
+                     stream=0):
+        """prefill on raw projections: K/Q prep, attention, gate (+ the int8 o_proj units)."""
+        _check(lib().mk_kv_prefill_prep(self.h, seq, layer0, n_layers, pos, T, k_ptr, v_ptr, knorm_ptr, qg_ptr, qnorm_ptr, out_ptr,
+                                        q32a or None, q32b or None, ctypes.cast(q32meta, _P_u16) if q32meta else None, stream))
 
     def rewind(self, seq, pos):
         _check(lib().mk_kv_rewind(self.h, seq, pos))

@@ -202,6 +202,29 @@ def bench_cfg5(torch, qkv, steps, warmup):
             "bytes_per_step": b}
 
 
+def bench_prefill(torch, qkv, steps, warmup):
+    """Prefill of a 16,384-position prompt in one call (640-bucket pieces inside) over 4 preset-F layers: K/V store +
+    causal attention.  FLOPs counted as the causal S and P V products (4 * 256 per visible (row, key) pair)."""
+    P, nl, win = 16384, 4, 2048
+    st = qkv.KVStore("K*=5r,V*=6", win=win, n_layers=nl, ctx=P)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(6)
+    k = torch.randn(P, nl, NKV, HD, device="cuda", dtype=torch.float16, generator=g)
+    v = torch.randn(P, nl, NKV, HD, device="cuda", dtype=torch.float16, generator=g)
+    q = torch.randn(nl, P, NH, HD, device="cuda", generator=g)
+    out = torch.empty_like(q)
+
+    def step():
+        st.rewind(0, 0)
+        st.prefill(0, 0, nl, 0, P, k.data_ptr(), v.data_ptr(), 1, q.data_ptr(), out.data_ptr())
+
+    t = timed(torch, step, steps, warmup)
+    pairs = NH * P * (P + 1) / 2  # visible (query row, key) pairs per layer
+    flops = nl * 4 * HD * pairs
+    return {"prompt": P, "layers": nl, "step_s": t, "tokens_per_s": P / t, "ms_per_layer": t / nl * 1e3,
+            "attn_tflops": flops / t / 1e12, "finite": bool(torch.isfinite(out).all().item())}
+
+
 def cpu_baseline(qkv, seconds=10.0):
     """The oracle (kv_oracle.c, the reference's split-K arithmetic restated in C) on host cores: layer 0 of config 3
     (101,600 positions, 4 kv heads, 24 query heads, T = 1) on dequantized operands, repeated for ~`seconds`."""
@@ -270,7 +293,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--configs", default="1,2,3,4,5")
+    ap.add_argument("--configs", default="1,2,3,4,5,6")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -304,6 +327,8 @@ def main():
         extra["cfg4"] = bench_cfg4(torch, qkv, args.steps, args.warmup)
     if 5 in cfgs:
         extra["cfg5"] = bench_cfg5(torch, qkv, args.steps, args.warmup)
+    if 6 in cfgs:
+        extra["prefill"] = bench_prefill(torch, qkv, min(args.steps, 3), min(args.warmup, 1))
     c3 = extra.get("cfg3")
     cpu = None if args.no_cpu or 3 not in cfgs else cpu_baseline(qkv, args.cpu_seconds)
     if cpu:

@@ -64,13 +64,13 @@ constexpr int PF_SEG = 8192; // key positions per prefill segment (a multiple of
 constexpr int PF_ROWS = 64;  // query rows per prefill workgroup (16 per wave)
 constexpr int PF_NS = 3;     // tile stages of a prefill workgroup (two tiles in flight)
 
-// canonical segment length: 32 * max(4, ceil(Lb / 4096)) with Lb = L rounded up to a 640 bucket, so at most 128
-// segments per kv head (one layer's 4 heads fill 2 workgroups on each of the 256 CUs) and the same partition for every
-// row count T whose rows share one bucket
+// canonical segment length: 128 ceil(Lb / 16384) positions with Lb = L rounded up to a 640 bucket: a multiple of 4 tiles,
+// so the 4 waves of a workgroup stream the same number of tiles; at most 128 segments per kv head (one layer's 4 heads
+// fit the 2 workgroup slots of each of the 256 CUs in one pass) and the same partition for every row count T whose rows
+// share one bucket
 inline __host__ __device__ int seg_len(int L) {
     const int lb = (L + ATT_BUCKET - 1) / ATT_BUCKET * ATT_BUCKET;
-    const int u = (lb + 4095) / 4096;
-    return ATP * (u > 4 ? u : 4);
+    return ATP * AWAVES * ((lb + 16383) / 16384);
 }
 constexpr int MAX_SEG = 128;
 constexpr int STAGE_BYTES = 2 * 32 * 256 + 1024; // one 32-position tile, widest format (q8 K and V) + its scales

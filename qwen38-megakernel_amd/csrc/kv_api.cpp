@@ -589,7 +589,7 @@ static int prefill_impl(void * h, int seq, int layer0, int n_layers, int pos, in
             p.L = n0 + Tp;
             p.ws = window_start(p.L, s.win);
             p.R = GQA * Tp;
-            p.nrb = (p.R + PF_ROWS - 1) / PF_ROWS;
+            p.nrb = (p.R + PF2_ROWS - 1) / PF2_ROWS;
             p.nseg = (p.L + PF_SEG - 1) / PF_SEG;
             p.qs = qs;
             p.gs = gs;

@@ -848,38 +848,100 @@ hipError_t launch_combine(const AttnArgs & a, hipStream_t st, hipEvent_t ev0, hi
 
 // ------------------------------------------------------------------------------------------------ prefill
 // Causal attention of one prefill piece (pk_attn8's exact form, prefill_attn.cuh:698-702; pieces and window
-// prefill_host.cu:606-615).  Workgroup = (64 query rows, kv head, key segment k of PF_SEG positions), row block
-// fastest so the workgroups of one segment run side by side.  Tiles are staged once per workgroup (PF_NS stages,
-// tile i copied by wave i % 4, two tiles in flight) and every wave runs compute_tile for its 16 rows on the shared
-// stage.  A row's partial for segment k is one online softmax over the segment's tiles in order, and the combine folds
-// a row's segments 0 .. pos / PF_SEG in order: each output is a function of its position and the store only, whatever
-// the chunking of the prefill.
+// prefill_host.cu:606-615).  Keys are cut into absolute segments of PF_SEG positions; a row's partial for segment k is
+// one online softmax over the segment's tiles in order, and the combine folds the row's segments 0 .. pos / PF_SEG in
+// order: each output is a function of its position and the store only, whatever the chunking of the prefill.
+
+// 32 values of scale block b (dims 32 b .. 32 b + 31) of one staged row of B bits -> 16 fp16 pairs fp16_rn(d q), the
+// same values as the decode operands (kfrag)
+template <int B>
+__device__ __forceinline__ void dequant_block(const uint8_t * row, uint16_t sc, int b, half2v (&o)[16]) {
+    const half2v d2 = as_h2((unsigned) sc * 0x10001u);
+    constexpr float bias = B == 8 ? 1152.f : (float) (1024 + (1 << (B - 1)));
+    const half2v b2 = {(_Float16) -bias, (_Float16) -bias};
+#pragma unroll
+    for (int w = 0; w < 4; w++) {
+        unsigned lo, hi;
+        if constexpr (B == 8) {
+            const uint2 x = *reinterpret_cast<const uint2 *>(row + 32 * b + 8 * w);
+            lo = x.x ^ 0x80808080u;
+            hi = x.y ^ 0x80808080u;
+        } else {
+            constexpr int HB = B - 4;
+            const int word = 4 * b + w;
+            const unsigned W = *reinterpret_cast<const unsigned *>(row + 4 * word);
+            unsigned H = 0;
+#pragma unroll
+            for (int k = 0; k < HB; k++) H |= (unsigned) row[128 + word * HB + k] << (8 * k);
+            word_codes<B>(W, H, lo, hi);
+        }
+        o[4 * w] = (as_h2(perm_b32(lo, C64, 0x00050004u)) + b2) * d2;
+        o[4 * w + 1] = (as_h2(perm_b32(lo, C64, 0x00070006u)) + b2) * d2;
+        o[4 * w + 2] = (as_h2(perm_b32(hi, C64, 0x00050004u)) + b2) * d2;
+        o[4 * w + 3] = (as_h2(perm_b32(hi, C64, 0x00070006u)) + b2) * d2;
+    }
+}
+
+// the staged tile (raw rows in stage `st`) -> fp16 K [32][SK_LD] and V transposed [256][SVT_LD] with the position order of
+// the P V operands (position bits 2 and 3 swapped).  Thread t: position t % 32, scale block t / 32.
+constexpr int SK_LD = HD + 8;
+constexpr int SVT_LD = ATP + 8;
 template <int KB, int VB>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void k_prefill(PrefillArgs a) {
+__device__ __forceinline__ void dequant_tile(const uint8_t * st, _Float16 * sK, _Float16 * sVt) {
+    const int p = threadIdx.x & 31, b = threadIdx.x >> 5;
+    const uint16_t * ksc = reinterpret_cast<const uint16_t *>(st + 1024 * (KB + VB));
+    const uint16_t * vsc = ksc + 8 * ATP;
+    half2v o[16];
+    dequant_block<KB>(st + p * 32 * KB, ksc[p * 8 + b], b, o);
+    uint4 * kd = reinterpret_cast<uint4 *>(sK + p * SK_LD + 32 * b);
+#pragma unroll
+    for (int k = 0; k < 4; k++) kd[k] = make_uint4(as_u(o[4 * k]), as_u(o[4 * k + 1]), as_u(o[4 * k + 2]), as_u(o[4 * k + 3]));
+    dequant_block<VB>(st + 1024 * KB + p * 32 * VB, vsc[p * 8 + b], b, o);
+    const int x = (p & ~12) | ((p >> 1) & 4) | ((p << 1) & 8);
+    _Float16 * vd = sVt + (32 * b) * SVT_LD + x;
+#pragma unroll
+    for (int k = 0; k < 16; k++) {
+        vd[(2 * k) * SVT_LD] = o[k][0];
+        vd[(2 * k + 1) * SVT_LD] = o[k][1];
+    }
+}
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+// Prefill attention on 32x32x16 MFMAs: workgroup = (128 query rows, kv head, key segment), row block fastest so the
+// workgroups of one segment run side by side; wave w = rows 32 w .. 32 w + 31.
+// Per 32-position tile the workgroup dequantizes the staged rows once into LDS (fp16 K, transposed V), then every wave
+// computes S^T = K Q^T (A = K rows from LDS, B = its query rows held in registers), the online softmax of its rows
+// (lane l: row l % 32, 16 of the 32 positions; lane l ^ 32 the other 16) and O^T += V^T P^T with P taken straight from
+// the S^T accumulators.  The same segments, partials and combine as k_prefill: each output a function of its position.
+template <int KB, int VB>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_prefill2(PrefillArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63, n = lane & 15, q = lane >> 4;
+    constexpr int NS = 2;
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63, c = lane & 31, hf = lane >> 5;
     const StoreLayout & S = a.S;
-    int b = blockIdx.x;
-    const int rb = b % a.nrb;
-    b /= a.nrb;
-    const int g = b % NKV, k = b / NKV;
-    const int r0 = PF_ROWS * rb, rlast = min(a.R, r0 + PF_ROWS) - 1;
-    const int pmax = a.n0 + rlast / GQA; // the last position any row of the block sees
+    int bi = blockIdx.x;
+    const int rb = bi % a.nrb;
+    bi /= a.nrb;
+    const int g = bi % NKV, k = bi / NKV;
+    const int r0 = PF2_ROWS * rb, rlast = min(a.R, r0 + PF2_ROWS) - 1;
+    const int pmax = a.n0 + rlast / GQA;
     const int c0 = k * PF_SEG;
-    if (c0 > pmax) return; // (no row of the block reads this segment: the combine skips it too)
+    if (c0 > pmax) return;
     const int c1 = min(c0 + PF_SEG, pmax + 1);
     const int ntiles = (c1 - c0 + ATP - 1) / ATP;
     const unsigned lds0 = (unsigned) (size_t) (__attribute__((address_space(3))) uint8_t *) smem;
-    half8 * const sQ = reinterpret_cast<half8 *>(smem + PF_NS * STAGE_BYTES); // [64][256] fp16, chunk-swizzled
+    _Float16 * const sK = reinterpret_cast<_Float16 *>(smem + NS * STAGE_BYTES);
+    _Float16 * const sVt = sK + ATP * SK_LD;
     const SideLayout & SK = S.side[a.layer][0];
     const SideLayout & SV = S.side[a.layer][1];
     const size_t ring0 = (size_t) (a.seq * NKV + g) * S.kvrc;
     const int L = a.L, ws = a.ws;
-
+    auto is_ring = [&](int i) { return S.kvrc > 0 && c0 + ATP * i >= ws; };
     auto issue = [&](int i) {
         const int p0 = c0 + ATP * i, nv = min(ATP, L - p0);
-        const unsigned lds = (unsigned) __builtin_amdgcn_readfirstlane(lds0 + (i % PF_NS) * STAGE_BYTES);
-        const bool ring = S.kvrc > 0 && p0 >= ws;
+        const unsigned lds = (unsigned) __builtin_amdgcn_readfirstlane(lds0 + (i % NS) * STAGE_BYTES);
+        const bool ring = is_ring(i);
         TileSrc t;
         size_t mr = 0;
         if (!ring || !SK.ring || !SV.ring) mr = attn_main_row(S, a.seq, g, p0);
@@ -901,79 +963,120 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         if (ring) issue_tile<8, 8>(t, nv, lds, lane);
         else issue_tile<KB, VB>(t, nv, lds, lane);
     };
-    // the first two tiles stream in while the query rows are prepared
-    if (wv == 0 && ntiles > 0) issue(0);
-    if (wv == 1 && ntiles > 1) issue(1);
-    const bool krot = a.krot;
-    for (int j = 0; j < 16; j++) {
-        const int rl = 16 * wv + j, r = r0 + rl;
-        half2v o0 = {(_Float16) 0.f, (_Float16) 0.f}, o1 = o0;
-        if (r < a.R) {
-            const int t = r / GQA, hh = r - GQA * t;
-            const float4 x = *reinterpret_cast<const float4 *>(a.q + ((size_t) t * NH + GQA * g + hh) * a.qs + 4 * lane);
-            float v[4] = {x.x, x.y, x.z, x.w};
-            if (a.qnw) qk_prep(v, a.qnw, a.rope + (size_t) (a.n0 + t) * 32);
-            if (krot) fwht256_w64(v);
-            o0[0] = (_Float16) (v[0] * 0.0625f);
-            o0[1] = (_Float16) (v[1] * 0.0625f);
-            o1[0] = (_Float16) (v[2] * 0.0625f);
-            o1[1] = (_Float16) (v[3] * 0.0625f);
+    // ---- the wave's 32 query rows: prep, FWHT for rotated K, * 1/16, fp16 through LDS into B fragments
+    {
+        _Float16 * const qs = reinterpret_cast<_Float16 *>(smem) + wv * 32 * SK_LD;
+        for (int j = 0; j < 32; j++) {
+            const int r = r0 + 32 * wv + j;
+            half2v o0 = {(_Float16) 0.f, (_Float16) 0.f}, o1 = o0;
+            if (r < a.R) {
+                const int t = r / GQA, hh = r - GQA * t;
+                const float4 x = *reinterpret_cast<const float4 *>(a.q + ((size_t) t * NH + GQA * g + hh) * a.qs + 4 * lane);
+                float v[4] = {x.x, x.y, x.z, x.w};
+                if (a.qnw) qk_prep(v, a.qnw, a.rope + (size_t) (a.n0 + t) * 32);
+                if (a.krot) fwht256_w64(v);
+                o0[0] = (_Float16) (v[0] * 0.0625f);
+                o0[1] = (_Float16) (v[1] * 0.0625f);
+                o1[0] = (_Float16) (v[2] * 0.0625f);
+                o1[1] = (_Float16) (v[3] * 0.0625f);
+            }
+            *reinterpret_cast<uint2 *>(qs + j * SK_LD + 4 * lane) = make_uint2(as_u(o0), as_u(o1));
         }
-        reinterpret_cast<uint2 *>(sQ + qchunk(rl, lane >> 1))[lane & 1] = make_uint2(as_u(o0), as_u(o1));
-    }
-    WaveState<2> st;
-#pragma unroll
-    for (int h = 0; h < 2; h++) {
-        st.m[h] = -INFINITY;
-        st.l[h] = 0.f;
-        const int r = r0 + 16 * wv + 8 * h + (n >> 1);
-        st.lim[h] = r < a.R ? a.n0 + r / GQA : -1;
-#pragma unroll
-        for (int bb = 0; bb < 8; bb++) st.acc[h][bb] = f32x4{0.f, 0.f, 0.f, 0.f};
-    }
-    st.lim_min = a.n0 + (r0 + 16 * wv) / GQA; // (padding rows: zero queries, their scores are never read)
-    const half8 * const sQw = sQ + 16 * wv * (HD / 8);
-    for (int i = 0; i < ntiles; i++) {
-        if (wv == i % 4) vm_wait<0>(); // the copies of tile i have landed (the wave's only ones in flight)
-        __syncthreads();               // tile i visible to every wave; every wave is done with tile i - 1's stage
-        if (i + 2 < ntiles && wv == (i + 2) % 4) issue(i + 2);
-        const uint8_t * const stp = smem + (i % PF_NS) * STAGE_BYTES;
-        const int p0 = c0 + ATP * i;
-        if (S.kvrc > 0 && p0 >= ws) {
-            RawTile<8, 8> raw;
-            read_k<8, 8>(raw, stp, n, q);
-            read_v<8, 8>(raw, stp, n, q);
-            lds_drain();
-            compute_tile<2, 8, 8>(st, sQw, p0, raw);
-        } else {
-            RawTile<KB, VB> raw;
-            read_k<KB, VB>(raw, stp, n, q);
-            read_v<KB, VB>(raw, stp, n, q);
-            lds_drain();
-            compute_tile<2, KB, VB>(st, sQw, p0, raw);
-        }
-    }
-    // ---- the wave's 16 partial rows: O through an LDS buffer of its own (coalesced rows), (m, l) per row
-    constexpr int OLD = HD + 4;
-    static_assert(AWAVES * 16 * OLD * 4 <= PF_NS * STAGE_BYTES + PF_ROWS * HD * 2, "prefill row buffers");
-    __syncthreads(); // every wave is done with the stages and the query rows
-    float * const ob = reinterpret_cast<float *>(smem) + wv * 16 * OLD;
-    const size_t unit = (size_t) (g * a.nseg + k) * a.R;
-#pragma unroll
-    for (int h = 0; h < 2; h++) {
-        float * o = ob + (8 * h + (n >> 1)) * OLD + 64 * q + (n & 1);
-#pragma unroll
-        for (int bb = 0; bb < 8; bb++)
-#pragma unroll
-            for (int i = 0; i < 4; i++) o[16 * i + 2 * bb] = st.acc[h][bb][i];
-        const int r = r0 + 16 * wv + 8 * h + (n >> 1);
-        if (q == 0 && !(n & 1) && r < a.R) a.ml[unit + r] = make_float2(st.m[h], st.l[h]);
     }
     __syncthreads();
-    for (int j = 0; j < 16; j++) {
-        const int r = r0 + 16 * wv + j;
-        if (r < a.R)
-            *reinterpret_cast<float4 *>(a.part + (unit + r) * HD + 4 * lane) = *reinterpret_cast<const float4 *>(ob + j * OLD + 4 * lane);
+    half8 qf[16];
+    {
+        const _Float16 * const qs = reinterpret_cast<const _Float16 *>(smem) + wv * 32 * SK_LD;
+#pragma unroll
+        for (int ks = 0; ks < 16; ks++) qf[ks] = *reinterpret_cast<const half8 *>(qs + c * SK_LD + 16 * ks + 8 * hf);
+    }
+    __syncthreads(); // the staging area is reused by the tiles
+    if (wv == 0 && ntiles > 0) issue(0);
+    const int row = r0 + 32 * wv + c;
+    const int lim = row < a.R ? a.n0 + row / GQA : -1;
+    const int lim_min = a.n0 + (r0 + 32 * wv) / GQA; // the wave's first row sees the fewest positions
+    float m = -INFINITY, l = 0.f;
+    f32x16 O[8];
+#pragma unroll
+    for (int db = 0; db < 8; db++)
+#pragma unroll
+        for (int e = 0; e < 16; e++) O[db][e] = 0.f;
+    constexpr float RESCALE_LOG2 = 8.f;
+    for (int i = 0; i < ntiles; i++) {
+        if (wv == i % 4) vm_wait<0>(); // tile i's copies (issued by this wave) have landed
+        __syncthreads();               // tile i visible; every wave is done with the fp16 tile i - 1
+        if (i + 1 < ntiles && wv == (i + 1) % 4) issue(i + 1);
+        const uint8_t * const stp = smem + (i % NS) * STAGE_BYTES;
+        if (is_ring(i)) dequant_tile<8, 8>(stp, sK, sVt);
+        else dequant_tile<KB, VB>(stp, sK, sVt);
+        __syncthreads(); // the fp16 tile is complete
+        const int p0 = c0 + ATP * i;
+        // ---- S^T = K Q^T: element 4 j + e = score of position 8 j + 4 hf + e for row c
+        f32x16 sacc;
+#pragma unroll
+        for (int e = 0; e < 16; e++) sacc[e] = 0.f;
+#pragma unroll
+        for (int ks = 0; ks < 16; ks++) {
+            const half8 ak = *reinterpret_cast<const half8 *>(sK + c * SK_LD + 16 * ks + 8 * hf);
+            sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(ak, qf[ks], sacc, 0, 0, 0);
+        }
+        const bool full = p0 + ATP - 1 <= lim_min;
+        float t[16];
+        float mx = -INFINITY;
+#pragma unroll
+        for (int e = 0; e < 16; e++) {
+            const int pos = p0 + 8 * (e >> 2) + 4 * hf + (e & 3);
+            const float sv = sacc[e] * LOG2E;
+            t[e] = full || pos <= lim ? sv : -INFINITY;
+            mx = fmaxf(mx, t[e]);
+        }
+        mx = fmaxf(mx, shfl_xor(mx, 32));
+        const float mnew = mx > m + RESCALE_LOG2 ? mx : m;
+        float al = 1.f, ps = 0.f, pv[16];
+        if (mnew != -INFINITY) {
+            al = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - mnew);
+#pragma unroll
+            for (int e = 0; e < 16; e++) {
+                pv[e] = __builtin_amdgcn_exp2f(t[e] - mnew);
+                ps += pv[e];
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 16; e++) pv[e] = 0.f;
+        }
+        ps += shfl_xor(ps, 32);
+        const bool rescale = al != 1.f && m != -INFINITY;
+        l = __builtin_fmaf(l, al, ps);
+        m = mnew;
+        if (__any(rescale)) {
+#pragma unroll
+            for (int db = 0; db < 8; db++) O[db] *= al;
+        }
+        half8 pb[2];
+#pragma unroll
+        for (int s2 = 0; s2 < 2; s2++)
+#pragma unroll
+            for (int e = 0; e < 8; e++) pb[s2][e] = (_Float16) pv[8 * s2 + e];
+        // ---- O^T += V^T P^T: dims 32 db + (row of A), positions of K step s2 in the permuted order
+#pragma unroll
+        for (int db = 0; db < 8; db++)
+#pragma unroll
+            for (int s2 = 0; s2 < 2; s2++) {
+                const half8 av = *reinterpret_cast<const half8 *>(sVt + (32 * db + c) * SVT_LD + 16 * s2 + 8 * hf);
+                O[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, pb[s2], O[db], 0, 0, 0);
+            }
+    }
+    // ---- partials: O^T element 4 j + e of block db = dim 32 db + 8 j + 4 hf + e of row c
+    if (row < a.R) {
+        const size_t u = (size_t) (g * a.nseg + k) * a.R + row;
+        if (hf == 0) a.ml[u] = make_float2(m, l);
+        float * const dst = a.part + u * HD;
+#pragma unroll
+        for (int db = 0; db < 8; db++)
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                *reinterpret_cast<float4 *>(dst + 32 * db + 8 * j + 4 * hf) =
+                    make_float4(O[db][4 * j], O[db][4 * j + 1], O[db][4 * j + 2], O[db][4 * j + 3]);
     }
 }
 
@@ -1059,11 +1162,11 @@ typedef void (*PrefillKernel)(PrefillArgs);
 static PrefillKernel pick_prefill(int kb, int vb) {
 #define QKV_VB(K)                                                                                                      \
     switch (vb) {                                                                                                      \
-    case 4: return k_prefill<K, 4>;                                                                                    \
-    case 5: return k_prefill<K, 5>;                                                                                    \
-    case 6: return k_prefill<K, 6>;                                                                                    \
-    case 7: return k_prefill<K, 7>;                                                                                    \
-    case 8: return k_prefill<K, 8>;                                                                                    \
+    case 4: return k_prefill2<K, 4>;                                                                                    \
+    case 5: return k_prefill2<K, 5>;                                                                                    \
+    case 6: return k_prefill2<K, 6>;                                                                                    \
+    case 7: return k_prefill2<K, 7>;                                                                                    \
+    case 8: return k_prefill2<K, 8>;                                                                                    \
     default: return nullptr;                                                                                           \
     }
     switch (kb) {
@@ -1080,7 +1183,8 @@ static PrefillKernel pick_prefill(int kb, int vb) {
 hipError_t launch_prefill(const PrefillArgs & a, int kb, int vb, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {
     PrefillKernel k = pick_prefill(kb, vb);
     if (!k) return hipErrorInvalidValue;
-    constexpr int lds = PF_NS * STAGE_BYTES + PF_ROWS * HD * 2;
+    constexpr int lds = 2 * STAGE_BYTES + (ATP * SK_LD + HD * SVT_LD) * 2;
+    static_assert(lds >= 4 * 32 * SK_LD * 2, "query staging inside the tile buffers");
     static thread_local const void * configured[32];
     static thread_local int n_configured = 0;
     bool done = false;

@@ -45,7 +45,7 @@ struct PrefillArgs {
     StoreLayout S;
     int layer, seq;
     int n0, Tp, L, ws; // first query position, rows' tokens, L = n0 + Tp (one 640-bucket), window start of the bucket
-    int R, nrb, nseg;  // 6 Tp rows per kv head, ceil(R / PF_ROWS) row blocks, ceil(L / PF_SEG) key segments
+    int R, nrb, nseg;  // 6 Tp rows per kv head, ceil(R / PF2_ROWS) row blocks, ceil(L / PF_SEG) key segments
     int krot, vrot;
     const float * q;   // [Tp][NH][qs]
     int qs;
@@ -60,9 +60,8 @@ struct PrefillArgs {
     float * part;      // [NKV][nseg][R][HD] per-segment partial outputs (unnormalised)
     float2 * ml;       // [NKV][nseg][R] (max in log2 units, sum)
 };
-constexpr int PF_SEG = 8192; // key positions per prefill segment (a multiple of 32)
-constexpr int PF_ROWS = 64;  // query rows per prefill workgroup (16 per wave)
-constexpr int PF_NS = 3;     // tile stages of a prefill workgroup (two tiles in flight)
+constexpr int PF_SEG = 4096; // key positions per prefill segment (a multiple of 32)
+constexpr int PF2_ROWS = 128; // query rows per prefill workgroup (32 per wave)
 
 // canonical segment length: 128 ceil(Lb / 16384) positions with Lb = L rounded up to a 640 bucket: a multiple of 4 tiles,
 // so the 4 waves of a workgroup stream the same number of tiles; at most 128 segments per kv head (one layer's 4 heads

@@ -882,23 +882,57 @@ __device__ __forceinline__ void dequant_block(const uint8_t * row, uint16_t sc, 
     }
 }
 
-// the staged tile (raw rows in stage `st`) -> fp16 K [32][SK_LD] and V transposed [256][SVT_LD] with the position order of
-// the P V operands (position bits 2 and 3 swapped).  Thread t: position t % 32, scale block t / 32.
+// fp16 tile layouts in LDS: K [32][SK_LD] (row = position), V transposed [256][SVT_LD] (row = dim) with the positions in
+// the order of the P V operands (position bits 2 and 3 swapped)
 constexpr int SK_LD = HD + 8;
 constexpr int SVT_LD = ATP + 8;
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+// Prefill attention on 32x32x16 MFMAs: workgroup = (128 query rows, kv head, key segment), row block fastest so the
+// workgroups of one segment run side by side; 8 waves.  Waves 0-3 (consumers) hold 32 query
+// rows each and run the MFMAs and the softmax on the fp16 tile of buffer i % 2; waves 4-7 (producers) each copy an
+// 8-position quarter of the tiles (two tiles in flight) and dequantize exactly what they copied into the other
+// buffer.  One barrier per tile hands a buffer over; on each SIMD a producer's VALU work overlaps a consumer's MFMAs.
+constexpr int PQ_REGION = 5120;                           // per producer and stage: K rows 2 KB, V rows 2 KB, scales 1 KB
+constexpr int PQ_STAGES = 2 * 4 * PQ_REGION;              // two stages of the 4 producers
+constexpr int PQ_BUF = (ATP * SK_LD + HD * SVT_LD + 64) * 2; // one fp16 tile: K [32][SK_LD], V^T [256][SVT_LD] + skew
+// V^T row r starts at r SVT_LD + 8 (r / 32): the 8 rows a producer wave writes at once (32 apart) fall in different banks
+constexpr int PQ_LDS = PQ_STAGES + 2 * PQ_BUF;
+static_assert(PQ_LDS >= PF2_ROWS * SK_LD * 2, "query staging inside the tile buffers");
+
+// the 8 positions of quarter pw of tile i: one producer wave's copies (5 instructions, always) into its region
 template <int KB, int VB>
-__device__ __forceinline__ void dequant_tile(const uint8_t * st, _Float16 * sK, _Float16 * sVt) {
-    const int p = threadIdx.x & 31, b = threadIdx.x >> 5;
-    const uint16_t * ksc = reinterpret_cast<const uint16_t *>(st + 1024 * (KB + VB));
-    const uint16_t * vsc = ksc + 8 * ATP;
+__device__ __forceinline__ void pq_issue(const TileSrc & t, int nq, unsigned lds, int lane) {
+    constexpr int KRB = 32 * KB, VRB = 32 * VB; // row bytes
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        int o = 1024 * j + 16 * lane;
+        if (o >= nq * KRB) o = nq * KRB - 16;
+        dma16(t.k + o, lds + 1024 * j);
+    }
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        int o = 1024 * j + 16 * lane;
+        if (o >= nq * VRB) o = nq * VRB - 16;
+        dma16(t.v + o, lds + 2048 + 1024 * j);
+    }
+    const int r = min(lane & 7, nq - 1);
+    dma16(lane < 8 ? static_cast<const void *>(t.ks + 8 * r) : static_cast<const void *>(t.vs + 8 * r), lds + 4096);
+}
+
+// one producer lane: position lane % 8 of its quarter, scale block lane / 8, K and V into the fp16 buffer
+template <int KB, int VB>
+__device__ __forceinline__ void pq_dequant(const uint8_t * reg, int pw, int lane, _Float16 * sK, _Float16 * sVt) {
+    const int pl = lane & 7, b = lane >> 3, p = 8 * pw + pl;
+    const uint16_t * ksc = reinterpret_cast<const uint16_t *>(reg + 4096);
     half2v o[16];
-    dequant_block<KB>(st + p * 32 * KB, ksc[p * 8 + b], b, o);
+    dequant_block<KB>(reg + pl * 32 * KB, ksc[pl * 8 + b], b, o);
     uint4 * kd = reinterpret_cast<uint4 *>(sK + p * SK_LD + 32 * b);
 #pragma unroll
     for (int k = 0; k < 4; k++) kd[k] = make_uint4(as_u(o[4 * k]), as_u(o[4 * k + 1]), as_u(o[4 * k + 2]), as_u(o[4 * k + 3]));
-    dequant_block<VB>(st + 1024 * KB + p * 32 * VB, vsc[p * 8 + b], b, o);
+    dequant_block<VB>(reg + 2048 + pl * 32 * VB, ksc[64 + pl * 8 + b], b, o);
     const int x = (p & ~12) | ((p >> 1) & 4) | ((p << 1) & 8);
-    _Float16 * vd = sVt + (32 * b) * SVT_LD + x;
+    _Float16 * vd = sVt + (32 * b) * SVT_LD + 8 * b + x;
 #pragma unroll
     for (int k = 0; k < 16; k++) {
         vd[(2 * k) * SVT_LD] = o[k][0];
@@ -906,19 +940,12 @@ __device__ __forceinline__ void dequant_tile(const uint8_t * st, _Float16 * sK, 
     }
 }
 
-typedef float f32x16 __attribute__((ext_vector_type(16)));
-
-// Prefill attention on 32x32x16 MFMAs: workgroup = (128 query rows, kv head, key segment), row block fastest so the
-// workgroups of one segment run side by side; wave w = rows 32 w .. 32 w + 31.
-// Per 32-position tile the workgroup dequantizes the staged rows once into LDS (fp16 K, transposed V), then every wave
-// computes S^T = K Q^T (A = K rows from LDS, B = its query rows held in registers), the online softmax of its rows
-// (lane l: row l % 32, 16 of the 32 positions; lane l ^ 32 the other 16) and O^T += V^T P^T with P taken straight from
-// the S^T accumulators.  The same segments, partials and combine as k_prefill: each output a function of its position.
 template <int KB, int VB>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_prefill2(PrefillArgs a) {
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_prefill3(PrefillArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    constexpr int NS = 2;
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63, c = lane & 31, hf = lane >> 5;
+    const bool producer = wv >= 4;
+    const int pw = wv - 4;
     const StoreLayout & S = a.S;
     int bi = blockIdx.x;
     const int rb = bi % a.nrb;
@@ -931,16 +958,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const int c1 = min(c0 + PF_SEG, pmax + 1);
     const int ntiles = (c1 - c0 + ATP - 1) / ATP;
     const unsigned lds0 = (unsigned) (size_t) (__attribute__((address_space(3))) uint8_t *) smem;
-    _Float16 * const sK = reinterpret_cast<_Float16 *>(smem + NS * STAGE_BYTES);
-    _Float16 * const sVt = sK + ATP * SK_LD;
+    _Float16 * const buf0 = reinterpret_cast<_Float16 *>(smem + PQ_STAGES);
     const SideLayout & SK = S.side[a.layer][0];
     const SideLayout & SV = S.side[a.layer][1];
     const size_t ring0 = (size_t) (a.seq * NKV + g) * S.kvrc;
     const int L = a.L, ws = a.ws;
     auto is_ring = [&](int i) { return S.kvrc > 0 && c0 + ATP * i >= ws; };
+    // producer: the copies of quarter pw of tile i into stage i % 2
     auto issue = [&](int i) {
-        const int p0 = c0 + ATP * i, nv = min(ATP, L - p0);
-        const unsigned lds = (unsigned) __builtin_amdgcn_readfirstlane(lds0 + (i % NS) * STAGE_BYTES);
+        const int p0t = c0 + ATP * i, nv = min(ATP, L - p0t);
+        const int q0 = min(8 * pw, nv - 1), nq = min(8, nv - q0), p0 = p0t + q0;
+        const unsigned lds = (unsigned) __builtin_amdgcn_readfirstlane(lds0 + ((i & 1) * 4 + pw) * PQ_REGION);
         const bool ring = is_ring(i);
         TileSrc t;
         size_t mr = 0;
@@ -960,41 +988,66 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             t.v = SV.vals + mr * (ring ? HD : 32 * VB);
             t.vs = SV.scs + mr * 8;
         }
-        if (ring) issue_tile<8, 8>(t, nv, lds, lane);
-        else issue_tile<KB, VB>(t, nv, lds, lane);
+        if (ring) pq_issue<8, 8>(t, nq, lds, lane);
+        else pq_issue<KB, VB>(t, nq, lds, lane);
     };
-    // ---- the wave's 32 query rows: prep, FWHT for rotated K, * 1/16, fp16 through LDS into B fragments
-    {
-        _Float16 * const qs = reinterpret_cast<_Float16 *>(smem) + wv * 32 * SK_LD;
-        for (int j = 0; j < 32; j++) {
-            const int r = r0 + 32 * wv + j;
-            half2v o0 = {(_Float16) 0.f, (_Float16) 0.f}, o1 = o0;
-            if (r < a.R) {
-                const int t = r / GQA, hh = r - GQA * t;
-                const float4 x = *reinterpret_cast<const float4 *>(a.q + ((size_t) t * NH + GQA * g + hh) * a.qs + 4 * lane);
-                float v[4] = {x.x, x.y, x.z, x.w};
-                if (a.qnw) qk_prep(v, a.qnw, a.rope + (size_t) (a.n0 + t) * 32);
-                if (a.krot) fwht256_w64(v);
-                o0[0] = (_Float16) (v[0] * 0.0625f);
-                o0[1] = (_Float16) (v[1] * 0.0625f);
-                o1[0] = (_Float16) (v[2] * 0.0625f);
-                o1[1] = (_Float16) (v[3] * 0.0625f);
-            }
-            *reinterpret_cast<uint2 *>(qs + j * SK_LD + 4 * lane) = make_uint2(as_u(o0), as_u(o1));
+    auto dequant = [&](int i) {
+        const uint8_t * reg = smem + ((i & 1) * 4 + pw) * PQ_REGION;
+        _Float16 * sK = buf0 + (i & 1) * (PQ_BUF / 2);
+        _Float16 * sVt = sK + ATP * SK_LD;
+        if (is_ring(i)) pq_dequant<8, 8>(reg, pw, lane, sK, sVt);
+        else pq_dequant<KB, VB>(reg, pw, lane, sK, sVt);
+    };
+    // ---- query rows: all 8 waves stage 16 rows each (prep, FWHT for rotated K, * 1/16, fp16), consumers take fragments
+    _Float16 * const qs = reinterpret_cast<_Float16 *>(smem);
+    for (int j = 0; j < 16; j++) {
+        const int rl = 16 * wv + j, r = r0 + rl;
+        half2v o0 = {(_Float16) 0.f, (_Float16) 0.f}, o1 = o0;
+        if (r < a.R) {
+            const int t = r / GQA, hh = r - GQA * t;
+            const float4 x = *reinterpret_cast<const float4 *>(a.q + ((size_t) t * NH + GQA * g + hh) * a.qs + 4 * lane);
+            float v[4] = {x.x, x.y, x.z, x.w};
+            if (a.qnw) qk_prep(v, a.qnw, a.rope + (size_t) (a.n0 + t) * 32);
+            if (a.krot) fwht256_w64(v);
+            o0[0] = (_Float16) (v[0] * 0.0625f);
+            o0[1] = (_Float16) (v[1] * 0.0625f);
+            o1[0] = (_Float16) (v[2] * 0.0625f);
+            o1[1] = (_Float16) (v[3] * 0.0625f);
         }
+        *reinterpret_cast<uint2 *>(qs + rl * SK_LD + 4 * lane) = make_uint2(as_u(o0), as_u(o1));
     }
     __syncthreads();
-    half8 qf[16];
-    {
-        const _Float16 * const qs = reinterpret_cast<const _Float16 *>(smem) + wv * 32 * SK_LD;
-#pragma unroll
-        for (int ks = 0; ks < 16; ks++) qf[ks] = *reinterpret_cast<const half8 *>(qs + c * SK_LD + 16 * ks + 8 * hf);
+    // Both roles pass the same barriers: two after the staging, then one per tile.
+    if (producer) {
+        __syncthreads(); // the consumers hold their query fragments: the staging area is free
+        issue(0);
+        if (ntiles > 1) issue(1);
+        if (ntiles > 1) vm_wait<5>();
+        else vm_wait<0>();
+        dequant(0);
+        lds_drain();
+        if (ntiles > 2) issue(2);
+        __syncthreads(); // buffer 0 complete
+        for (int i = 0; i < ntiles; i++) {
+            if (i + 1 < ntiles) {
+                if (i + 2 < ntiles) vm_wait<5>(); // tile i + 1 landed (tile i + 2 may be in flight)
+                else vm_wait<0>();
+                dequant(i + 1);
+                lds_drain();
+                if (i + 3 < ntiles) issue(i + 3);
+            }
+            __syncthreads(); // buffer (i + 1) % 2 complete, buffer i % 2 free
+        }
+        return;
     }
-    __syncthreads(); // the staging area is reused by the tiles
-    if (wv == 0 && ntiles > 0) issue(0);
+    half8 qf[16];
+#pragma unroll
+    for (int ks = 0; ks < 16; ks++) qf[ks] = *reinterpret_cast<const half8 *>(qs + (32 * wv + c) * SK_LD + 16 * ks + 8 * hf);
+    __syncthreads();
+    __syncthreads();
     const int row = r0 + 32 * wv + c;
     const int lim = row < a.R ? a.n0 + row / GQA : -1;
-    const int lim_min = a.n0 + (r0 + 32 * wv) / GQA; // the wave's first row sees the fewest positions
+    const int lim_min = a.n0 + (r0 + 32 * wv) / GQA;
     float m = -INFINITY, l = 0.f;
     f32x16 O[8];
 #pragma unroll
@@ -1003,15 +1056,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         for (int e = 0; e < 16; e++) O[db][e] = 0.f;
     constexpr float RESCALE_LOG2 = 8.f;
     for (int i = 0; i < ntiles; i++) {
-        if (wv == i % 4) vm_wait<0>(); // tile i's copies (issued by this wave) have landed
-        __syncthreads();               // tile i visible; every wave is done with the fp16 tile i - 1
-        if (i + 1 < ntiles && wv == (i + 1) % 4) issue(i + 1);
-        const uint8_t * const stp = smem + (i % NS) * STAGE_BYTES;
-        if (is_ring(i)) dequant_tile<8, 8>(stp, sK, sVt);
-        else dequant_tile<KB, VB>(stp, sK, sVt);
-        __syncthreads(); // the fp16 tile is complete
+        const _Float16 * const sK = buf0 + (i & 1) * (PQ_BUF / 2);
+        const _Float16 * const sVt = sK + ATP * SK_LD;
         const int p0 = c0 + ATP * i;
-        // ---- S^T = K Q^T: element 4 j + e = score of position 8 j + 4 hf + e for row c
         f32x16 sacc;
 #pragma unroll
         for (int e = 0; e < 16; e++) sacc[e] = 0.f;
@@ -1021,28 +1068,26 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(ak, qf[ks], sacc, 0, 0, 0);
         }
         const bool full = p0 + ATP - 1 <= lim_min;
-        float t[16];
         float mx = -INFINITY;
 #pragma unroll
         for (int e = 0; e < 16; e++) {
             const int pos = p0 + 8 * (e >> 2) + 4 * hf + (e & 3);
-            const float sv = sacc[e] * LOG2E;
-            t[e] = full || pos <= lim ? sv : -INFINITY;
-            mx = fmaxf(mx, t[e]);
+            sacc[e] = full || pos <= lim ? sacc[e] * LOG2E : -INFINITY;
+            mx = fmaxf(mx, sacc[e]);
         }
         mx = fmaxf(mx, shfl_xor(mx, 32));
         const float mnew = mx > m + RESCALE_LOG2 ? mx : m;
-        float al = 1.f, ps = 0.f, pv[16];
+        float al = 1.f, ps = 0.f;
         if (mnew != -INFINITY) {
             al = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - mnew);
 #pragma unroll
             for (int e = 0; e < 16; e++) {
-                pv[e] = __builtin_amdgcn_exp2f(t[e] - mnew);
-                ps += pv[e];
+                sacc[e] = __builtin_amdgcn_exp2f(sacc[e] - mnew);
+                ps += sacc[e];
             }
         } else {
 #pragma unroll
-            for (int e = 0; e < 16; e++) pv[e] = 0.f;
+            for (int e = 0; e < 16; e++) sacc[e] = 0.f;
         }
         ps += shfl_xor(ps, 32);
         const bool rescale = al != 1.f && m != -INFINITY;
@@ -1056,17 +1101,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
         for (int s2 = 0; s2 < 2; s2++)
 #pragma unroll
-            for (int e = 0; e < 8; e++) pb[s2][e] = (_Float16) pv[8 * s2 + e];
-        // ---- O^T += V^T P^T: dims 32 db + (row of A), positions of K step s2 in the permuted order
+            for (int e = 0; e < 8; e++) pb[s2][e] = (_Float16) sacc[8 * s2 + e];
 #pragma unroll
         for (int db = 0; db < 8; db++)
 #pragma unroll
             for (int s2 = 0; s2 < 2; s2++) {
-                const half8 av = *reinterpret_cast<const half8 *>(sVt + (32 * db + c) * SVT_LD + 16 * s2 + 8 * hf);
+                const half8 av = *reinterpret_cast<const half8 *>(sVt + (32 * db + c) * SVT_LD + 8 * db + 16 * s2 + 8 * hf);
                 O[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, pb[s2], O[db], 0, 0, 0);
             }
+        __syncthreads(); // buffer i % 2 free for the producers
     }
-    // ---- partials: O^T element 4 j + e of block db = dim 32 db + 8 j + 4 hf + e of row c
     if (row < a.R) {
         const size_t u = (size_t) (g * a.nseg + k) * a.R + row;
         if (hf == 0) a.ml[u] = make_float2(m, l);
@@ -1162,11 +1206,11 @@ typedef void (*PrefillKernel)(PrefillArgs);
 static PrefillKernel pick_prefill(int kb, int vb) {
 #define QKV_VB(K)                                                                                                      \
     switch (vb) {                                                                                                      \
-    case 4: return k_prefill2<K, 4>;                                                                                    \
-    case 5: return k_prefill2<K, 5>;                                                                                    \
-    case 6: return k_prefill2<K, 6>;                                                                                    \
-    case 7: return k_prefill2<K, 7>;                                                                                    \
-    case 8: return k_prefill2<K, 8>;                                                                                    \
+    case 4: return k_prefill3<K, 4>;                                                                                    \
+    case 5: return k_prefill3<K, 5>;                                                                                    \
+    case 6: return k_prefill3<K, 6>;                                                                                    \
+    case 7: return k_prefill3<K, 7>;                                                                                    \
+    case 8: return k_prefill3<K, 8>;                                                                                    \
     default: return nullptr;                                                                                           \
     }
     switch (kb) {
@@ -1183,8 +1227,7 @@ static PrefillKernel pick_prefill(int kb, int vb) {
 hipError_t launch_prefill(const PrefillArgs & a, int kb, int vb, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {
     PrefillKernel k = pick_prefill(kb, vb);
     if (!k) return hipErrorInvalidValue;
-    constexpr int lds = 2 * STAGE_BYTES + (ATP * SK_LD + HD * SVT_LD) * 2;
-    static_assert(lds >= 4 * 32 * SK_LD * 2, "query staging inside the tile buffers");
+    constexpr int lds = PQ_LDS;
     static thread_local const void * configured[32];
     static thread_local int n_configured = 0;
     bool done = false;
@@ -1194,7 +1237,7 @@ hipError_t launch_prefill(const PrefillArgs & a, int kb, int vb, hipStream_t st,
         if (e != hipSuccess) return e;
         if (n_configured < 32) configured[n_configured++] = (const void *) k;
     }
-    hipExtLaunchKernelGGL(k, dim3(a.nrb * NKV * a.nseg), dim3(256), lds, st, ev0, nullptr, 0, a);
+    hipExtLaunchKernelGGL(k, dim3(a.nrb * NKV * a.nseg), dim3(512), lds, st, ev0, nullptr, 0, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     hipExtLaunchKernelGGL(k_prefill_combine, dim3((a.R * NKV + 3) / 4), dim3(256), 0, st, nullptr, ev1, 0, a);

@@ -145,3 +145,30 @@ def test_prefill_errors(qkv, torch_gpu):
     torch.cuda.synchronize()
     assert np.all(np.isfinite(o.cpu().numpy()))
     st.close()
+
+
+def test_prefill_paged_equals_contiguous(qkv, torch_gpu):
+    """Prefill on a shared page pool with a permuted page table gives the contiguous store's outputs bit for bit."""
+    torch = torch_gpu
+    rng = np.random.default_rng(44)
+    P, nl, win, spec, page = 1500, 1, 512, "K*=5r,V*=6", 256
+    K, V = synth_kv(rng, P, nl, outliers=True)
+    Q = rng.standard_normal((nl, P, NH, HD)).astype(np.float32)
+    st, ref = run_prefill(qkv, torch, spec, win, K, V, Q, [900, 600], 2048)
+    st.close()
+    npg = 2048 // page
+    paged = qkv.KVStore(spec, win=win, n_layers=nl, n_seq=2, ctx=2048, page=page, n_pages=2 * npg)
+    perm = np.random.default_rng(7).permutation(2 * npg)
+    paged.set_pages(1, perm[:npg])
+    outs, p = [], 0
+    for c in (900, 600):
+        k = torch.from_numpy(np.ascontiguousarray(K[p:p + c])).cuda()
+        v = torch.from_numpy(np.ascontiguousarray(V[p:p + c])).cuda()
+        q = torch.from_numpy(np.ascontiguousarray(Q[:, p:p + c])).cuda()
+        o = torch.empty_like(q)
+        paged.prefill(1, 0, nl, p, c, k.data_ptr(), v.data_ptr(), 0, q.data_ptr(), o.data_ptr())
+        torch.cuda.synchronize()
+        outs.append(o.cpu().numpy())
+        p += c
+    assert np.array_equal(np.concatenate(outs, axis=1), ref)
+    paged.close()

@@ -1072,17 +1072,19 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         const _Float16 * const sK = buf0 + (i & 1) * (PQ_BUF / 2);
         const _Float16 * const sVt = sK + ATP * SK_LD;
         const int p0 = c0 + ATP * i;
-        f32x16 sacc, sacc1;
+        // K fragments read 4 ahead of their MFMAs (the LDS latency is the cost here, not the MFMA chain)
+        f32x16 sacc;
 #pragma unroll
-        for (int e = 0; e < 16; e++) sacc[e] = sacc1[e] = 0.f;
+        for (int e = 0; e < 16; e++) sacc[e] = 0.f;
+        half8 akf[4];
 #pragma unroll
-        for (int ks = 0; ks < 16; ks += 2) { // two accumulators: consecutive MFMAs do not wait on each other
-            const half8 ak0 = *reinterpret_cast<const half8 *>(sK + c * SK_LD + 16 * ks + 8 * hf);
-            const half8 ak1 = *reinterpret_cast<const half8 *>(sK + c * SK_LD + 16 * ks + 16 + 8 * hf);
-            sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(ak0, qf[ks], sacc, 0, 0, 0);
-            sacc1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(ak1, qf[ks + 1], sacc1, 0, 0, 0);
+        for (int ks = 0; ks < 4; ks++) akf[ks] = *reinterpret_cast<const half8 *>(sK + c * SK_LD + 16 * ks + 8 * hf);
+#pragma unroll
+        for (int ks = 0; ks < 16; ks++) {
+            const half8 ak = akf[ks & 3];
+            if (ks + 4 < 16) akf[ks & 3] = *reinterpret_cast<const half8 *>(sK + c * SK_LD + 16 * (ks + 4) + 8 * hf);
+            sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(ak, qf[ks], sacc, 0, 0, 0);
         }
-        sacc += sacc1;
         const bool full = p0 + ATP - 1 <= lim_min;
         float mx = -INFINITY;
 #pragma unroll
@@ -1118,13 +1120,20 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         for (int s2 = 0; s2 < 2; s2++)
 #pragma unroll
             for (int e = 0; e < 8; e++) pb[s2][e] = (_Float16) sacc[8 * s2 + e];
+        // V^T fragments j = 8 s2 + db, read 4 ahead of their MFMAs
+        auto vfrag = [&](int j) {
+            const int db = j & 7, s2 = j >> 3;
+            return *reinterpret_cast<const half8 *>(sVt + (32 * db + c) * SVT_LD + 8 * db + 16 * s2 + 8 * hf);
+        };
+        half8 avf[4];
 #pragma unroll
-        for (int s2 = 0; s2 < 2; s2++)
+        for (int j = 0; j < 4; j++) avf[j] = vfrag(j);
 #pragma unroll
-            for (int db = 0; db < 8; db++) {
-                const half8 av = *reinterpret_cast<const half8 *>(sVt + (32 * db + c) * SVT_LD + 8 * db + 16 * s2 + 8 * hf);
-                O[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, pb[s2], O[db], 0, 0, 0);
-            }
+        for (int j = 0; j < 16; j++) {
+            const half8 av = avf[j & 3];
+            if (j + 4 < 16) avf[j & 3] = vfrag(j + 4);
+            O[j & 7] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, pb[j >> 3], O[j & 7], 0, 0, 0);
+        }
         __syncthreads(); // buffer i % 2 free for the producers
     }
     if (row < a.R) {

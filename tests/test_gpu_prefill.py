@@ -172,3 +172,34 @@ def test_prefill_paged_equals_contiguous(qkv, torch_gpu):
         p += c
     assert np.array_equal(np.concatenate(outs, axis=1), ref)
     paged.close()
+
+
+@pytest.mark.parametrize("spec,win,win_all", [("K*=6r,V*=7", 640, 0), ("", 1024, 1)])
+def test_prefill_after_appends(qkv, oracle, torch_gpu, spec, win, win_all):
+    """Rows stored by decode-style appends, then a prefill chunk from that position (one-token piece included), then the
+    exact attention of the chunk's rows; q8 sides with their own ring (win_all) as well."""
+    torch = torch_gpu
+    rng = np.random.default_rng(45)
+    nl, P0, P = 1, 1279, 2000
+    K, V = synth_kv(rng, P, nl, outliers=True)
+    Q = rng.standard_normal((nl, P - P0, NH, HD)).astype(np.float32)
+    st = qkv.KVStore(spec, win=win, n_layers=nl, ctx=2048, win_all=win_all)
+    for p0, c in ((0, 1000), (1000, 279)):
+        k = torch.from_numpy(np.ascontiguousarray(K[p0:p0 + c])).cuda()
+        v = torch.from_numpy(np.ascontiguousarray(V[p0:p0 + c])).cuda()
+        st.append(0, 0, nl, p0, c, k.data_ptr(), v.data_ptr(), 0)
+    k = torch.from_numpy(np.ascontiguousarray(K[P0:])).cuda()
+    v = torch.from_numpy(np.ascontiguousarray(V[P0:])).cuda()
+    q = torch.from_numpy(Q).cuda()
+    o = torch.empty_like(q)
+    st.prefill(0, 0, nl, P0, P - P0, k.data_ptr(), v.data_ptr(), 0, q.data_ptr(), o.data_ptr())
+    torch.cuda.synchronize()
+    out = o.cpu().numpy()
+    kb, vb, kr, vr = st.kbits[0], st.vbits[0], st.krot[0], st.vrot[0]
+    ring_k = win > 0 and (kb != 8 or win_all)
+    ring_v = win > 0 and (vb != 8 or win_all)
+    for a, b in ((P0, 1280), (1280, 1920), (1920, P)):
+        ref = expected_attention(oracle, Q[0, a - P0:b - P0], K[:b, 0], V[:b, 0], b - a, kr, vr, kb, vb, qkv.window_start(b, win),
+                                 ring_k, ring_v)
+        assert rel_err(out[0, a - P0:b - P0], ref) <= 2e-3, (a, b)
+    st.close()

@@ -859,34 +859,21 @@ __device__ __forceinline__ void dequant_block(const uint8_t * row, uint16_t sc, 
     const half2v d2 = as_h2((unsigned) sc * 0x10001u);
     constexpr float bias = B == 8 ? 1152.f : (float) (1024 + (1 << (B - 1)));
     const half2v b2 = {(_Float16) -bias, (_Float16) -bias};
-    // the block's bytes in one or two wide reads: q8 32 bytes; packed 4 nibble words (16 bytes) + 4 HB-byte fields
-    unsigned Wd[8], Hf[3] = {0u, 0u, 0u};
-    if constexpr (B == 8) {
-        const uint4 x0 = reinterpret_cast<const uint4 *>(row + 32 * b)[0], x1 = reinterpret_cast<const uint4 *>(row + 32 * b)[1];
-        Wd[0] = x0.x; Wd[1] = x0.y; Wd[2] = x0.z; Wd[3] = x0.w; Wd[4] = x1.x; Wd[5] = x1.y; Wd[6] = x1.z; Wd[7] = x1.w;
-    } else {
-        constexpr int HB = B - 4;
-        const uint4 x = *reinterpret_cast<const uint4 *>(row + 16 * b);
-        Wd[0] = x.x; Wd[1] = x.y; Wd[2] = x.z; Wd[3] = x.w;
-        const unsigned * hp = reinterpret_cast<const unsigned *>(row + 128 + 4 * HB * b);
-        if constexpr (HB == 1) Hf[0] = hp[0];
-        if constexpr (HB == 2) { const uint2 y = *reinterpret_cast<const uint2 *>(hp); Hf[0] = y.x; Hf[1] = y.y; }
-        if constexpr (HB == 3) { Hf[0] = hp[0]; Hf[1] = hp[1]; Hf[2] = hp[2]; }
-    }
 #pragma unroll
     for (int w = 0; w < 4; w++) {
         unsigned lo, hi;
         if constexpr (B == 8) {
-            lo = Wd[2 * w] ^ 0x80808080u;
-            hi = Wd[2 * w + 1] ^ 0x80808080u;
+            const uint2 x = *reinterpret_cast<const uint2 *>(row + 32 * b + 8 * w);
+            lo = x.x ^ 0x80808080u;
+            hi = x.y ^ 0x80808080u;
         } else {
             constexpr int HB = B - 4;
-            // the HB-byte field of word w: bits 8 HB w .. of the little-endian 4 HB-byte run
-            const int bit = 8 * HB * w, dw = bit >> 5, sh = bit & 31;
-            unsigned H = Hf[dw] >> sh;
-            if (sh + 8 * HB > 32) H |= Hf[dw + 1] << (32 - sh);
-            H &= (1u << (8 * HB)) - 1u;
-            word_codes<B>(Wd[w], H, lo, hi);
+            const int word = 4 * b + w;
+            const unsigned W = *reinterpret_cast<const unsigned *>(row + 4 * word);
+            unsigned H = 0;
+#pragma unroll
+            for (int k = 0; k < HB; k++) H |= (unsigned) row[128 + word * HB + k] << (8 * k);
+            word_codes<B>(W, H, lo, hi);
         }
         o[4 * w] = (as_h2(perm_b32(lo, C64, 0x00050004u)) + b2) * d2;
         o[4 * w + 1] = (as_h2(perm_b32(lo, C64, 0x00070006u)) + b2) * d2;
@@ -1072,17 +1059,12 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         const _Float16 * const sK = buf0 + (i & 1) * (PQ_BUF / 2);
         const _Float16 * const sVt = sK + ATP * SK_LD;
         const int p0 = c0 + ATP * i;
-        // K fragments read 4 ahead of their MFMAs (the LDS latency is the cost here, not the MFMA chain)
         f32x16 sacc;
 #pragma unroll
         for (int e = 0; e < 16; e++) sacc[e] = 0.f;
-        half8 akf[4];
-#pragma unroll
-        for (int ks = 0; ks < 4; ks++) akf[ks] = *reinterpret_cast<const half8 *>(sK + c * SK_LD + 16 * ks + 8 * hf);
 #pragma unroll
         for (int ks = 0; ks < 16; ks++) {
-            const half8 ak = akf[ks & 3];
-            if (ks + 4 < 16) akf[ks & 3] = *reinterpret_cast<const half8 *>(sK + c * SK_LD + 16 * (ks + 4) + 8 * hf);
+            const half8 ak = *reinterpret_cast<const half8 *>(sK + c * SK_LD + 16 * ks + 8 * hf);
             sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(ak, qf[ks], sacc, 0, 0, 0);
         }
         const bool full = p0 + ATP - 1 <= lim_min;
@@ -1120,20 +1102,13 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         for (int s2 = 0; s2 < 2; s2++)
 #pragma unroll
             for (int e = 0; e < 8; e++) pb[s2][e] = (_Float16) sacc[8 * s2 + e];
-        // V^T fragments j = 8 s2 + db, read 4 ahead of their MFMAs
-        auto vfrag = [&](int j) {
-            const int db = j & 7, s2 = j >> 3;
-            return *reinterpret_cast<const half8 *>(sVt + (32 * db + c) * SVT_LD + 8 * db + 16 * s2 + 8 * hf);
-        };
-        half8 avf[4];
 #pragma unroll
-        for (int j = 0; j < 4; j++) avf[j] = vfrag(j);
+        for (int db = 0; db < 8; db++)
 #pragma unroll
-        for (int j = 0; j < 16; j++) {
-            const half8 av = avf[j & 3];
-            if (j + 4 < 16) avf[j & 3] = vfrag(j + 4);
-            O[j & 7] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, pb[j >> 3], O[j & 7], 0, 0, 0);
-        }
+            for (int s2 = 0; s2 < 2; s2++) {
+                const half8 av = *reinterpret_cast<const half8 *>(sVt + (32 * db + c) * SVT_LD + 8 * db + 16 * s2 + 8 * hf);
+                O[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, pb[s2], O[db], 0, 0, 0);
+            }
         __syncthreads(); // buffer i % 2 free for the producers
     }
     if (row < a.R) {

@@ -247,6 +247,33 @@ struct TileSrc {
     const uint16_t * vs;
 };
 
+// the source rows of the 32 positions from p0 (wave-uniform) of (seq, kv head g): window tiles (ring) are q8 rows
+// from the ring of sides that have one, else from the main store (q8 sides); other tiles are main-store rows of
+// KB / VB bits.  ring0 = the first ring row of (seq, g).
+template <int KB, int VB>
+__device__ __forceinline__ TileSrc tile_src(const StoreLayout & S, const SideLayout & SK, const SideLayout & SV, int seq, int g, int p0,
+                                           size_t ring0, bool ring) {
+    TileSrc t;
+    size_t mr = 0;
+    if (!ring || !SK.ring || !SV.ring) mr = attn_main_row(S, seq, g, p0);
+    const size_t rr = ring ? ring0 + __builtin_amdgcn_readfirstlane(p0 % max(S.kvrc, 1)) : 0;
+    if (ring && SK.ring) {
+        t.k = reinterpret_cast<const uint8_t *>(SK.ring) + rr * HD;
+        t.ks = SK.rsc + rr * 8;
+    } else {
+        t.k = SK.vals + mr * (ring ? HD : 32 * KB);
+        t.ks = SK.scs + mr * 8;
+    }
+    if (ring && SV.ring) {
+        t.v = reinterpret_cast<const uint8_t *>(SV.ring) + rr * HD;
+        t.vs = SV.rsc + rr * 8;
+    } else {
+        t.v = SV.vals + mr * (ring ? HD : 32 * VB);
+        t.vs = SV.scs + mr * 8;
+    }
+    return t;
+}
+
 // copies of one tile into the stage at LDS address `lds`; returns the number of copy instructions (KB + VB + 1).
 // Full tiles copy contiguous bytes (one address add per instruction); the last, partial tile of a context clamps each
 // 16-byte chunk to the last valid row.
@@ -496,24 +523,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NP == 1 ? 2
         auto issue = [&](int i) {
             const int p0 = c0 + ATP * (wv + AWAVES * i), nv = min(ATP, L - p0);
             const bool ring = S.kvrc > 0 && p0 >= ws; // the window: q8 rows (ring, or the main store of q8 sides)
-            TileSrc t;
-            size_t mr = 0;
-            if (!ring || !SK.ring || !SV.ring) mr = attn_main_row(S, seq, g, p0);
-            const size_t rr = ring ? ring0 + __builtin_amdgcn_readfirstlane(p0 % max(S.kvrc, 1)) : 0;
-            if (ring && SK.ring) {
-                t.k = reinterpret_cast<const uint8_t *>(SK.ring) + rr * HD;
-                t.ks = SK.rsc + rr * 8;
-            } else {
-                t.k = SK.vals + mr * (ring ? HD : 32 * KB);
-                t.ks = SK.scs + mr * 8;
-            }
-            if (ring && SV.ring) {
-                t.v = reinterpret_cast<const uint8_t *>(SV.ring) + rr * HD;
-                t.vs = SV.rsc + rr * 8;
-            } else {
-                t.v = SV.vals + mr * (ring ? HD : 32 * VB);
-                t.vs = SV.scs + mr * 8;
-            }
+            const TileSrc t = tile_src<KB, VB>(S, SK, SV, seq, g, p0, ring0, ring);
             if (ring) issue_tile<8, 8>(t, nv, st_lds, lane);
             else issue_tile<KB, VB>(t, nv, st_lds, lane);
         };
@@ -970,24 +980,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         const int q0 = min(8 * pw, nv - 1), nq = min(8, nv - q0), p0 = p0t + q0;
         const unsigned lds = (unsigned) __builtin_amdgcn_readfirstlane(lds0 + ((i & 1) * 4 + pw) * PQ_REGION);
         const bool ring = is_ring(i);
-        TileSrc t;
-        size_t mr = 0;
-        if (!ring || !SK.ring || !SV.ring) mr = attn_main_row(S, a.seq, g, p0);
-        const size_t rr = ring ? ring0 + __builtin_amdgcn_readfirstlane(p0 % max(S.kvrc, 1)) : 0;
-        if (ring && SK.ring) {
-            t.k = reinterpret_cast<const uint8_t *>(SK.ring) + rr * HD;
-            t.ks = SK.rsc + rr * 8;
-        } else {
-            t.k = SK.vals + mr * (ring ? HD : 32 * KB);
-            t.ks = SK.scs + mr * 8;
-        }
-        if (ring && SV.ring) {
-            t.v = reinterpret_cast<const uint8_t *>(SV.ring) + rr * HD;
-            t.vs = SV.rsc + rr * 8;
-        } else {
-            t.v = SV.vals + mr * (ring ? HD : 32 * VB);
-            t.vs = SV.scs + mr * 8;
-        }
+        const TileSrc t = tile_src<KB, VB>(S, SK, SV, a.seq, g, p0, ring0, ring);
         if (ring) pq_issue<8, 8>(t, nq, lds, lane);
         else pq_issue<KB, VB>(t, nq, lds, lane);
     };

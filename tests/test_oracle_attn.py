@@ -11,7 +11,7 @@ def test_window_spot_values(oracle):
     spans = {L - oracle.ws(L, 2048) for L in range(3201, 20000)}
     assert min(spans) == 2561 and max(spans) == 3200
     assert oracle.kvrc(2048) == 3232                     # loader.cu:1479-1486
-    assert oracle.ws(101600, 2048) == 98560               # SURVEY cfg 3: ring 3,040 / packed 98,560
+    assert oracle.ws(101600, 2048) == 98560               # L = 101,600, W = 2,048: ring 3,040 / packed 98,560
     assert [oracle.ws(L, 2048) for L in (23000, 60000, 262144)] == [19840, 56960, 259200]
     assert {oracle.kvrc(w) for w in range(1921, 2561)} == {3232}
     assert oracle.ws(5000, 0) == 0 and oracle.kvrc(0) == 0

@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the quantized KV-cache path on one MI355X (BASELINE.json's metric).
 
-Headline (`value`): BASELINE config 3 -- single-query decode attention at 101,600 context, preset F (K 5-bit
+Headline (`value`): the 101,600-context workload -- single-query decode attention at 101,600 context, preset F (K 5-bit
 Hadamard-rotated, V 6-bit, 2,048-position q8 window; the reference's window rule puts 3,040 positions in the ring and
 98,560 in the packed store), 16 layers x 4 kv heads x head_dim 256, 24 query heads.  One step = the 16 layers'
 attention (16 attend calls, one per layer, as a decoder issues them), inputs resident in HBM.

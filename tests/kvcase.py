@@ -6,7 +6,7 @@ HD, NKV, NH, GQA = 256, 4, 24, 6
 
 
 def synth_kv(rng, T, nl, outliers=False):
-    """K, V of shape [T][nl][4][256] fp32.  outliers: 4 channels per kv head scaled x12 (BASELINE configs 2/3)."""
+    """K, V of shape [T][nl][4][256] fp32.  outliers: 4 channels per kv head scaled x12 (the outlier-channel distribution of the append and 101,600-context workloads)."""
     K = rng.standard_normal((T, nl, NKV, HD)).astype(np.float32)
     V = rng.standard_normal((T, nl, NKV, HD)).astype(np.float32)
     if outliers:

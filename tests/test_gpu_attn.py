@@ -43,13 +43,13 @@ def check_case(qkv, oracle, torch, spec, win, L, T, nl=1, seed=0, outliers=False
 
 
 def test_cfg1_q8_4096(qkv, oracle, torch_gpu):
-    """all q8, one layer, 4,096 positions, one query token, seed 0."""
+    """The reference host path's workload: all q8, one layer, 4,096 positions, one query token, seed 0."""
     check_case(qkv, oracle, torch_gpu, "", 0, 4096, 1, seed=0)
 
 
 @pytest.mark.parametrize("spec", ["K*=5r,V*=6", "K*=5r,V*=5"])
 def test_preset_f_window(qkv, oracle, torch_gpu, spec):
-    """Preset F (BASELINE's K5r/V6 and the reference's K5r/V5) with the 2,048 window: mixed ring/packed tiles."""
+    """Preset F (K5r/V6 as benchmarked, and the reference's K5r/V5) with the 2,048 window: mixed ring/packed tiles."""
     check_case(qkv, oracle, torch_gpu, spec, 2048, 5000, 1, nl=2, seed=1, outliers=True)
 
 
@@ -59,7 +59,7 @@ def test_short_and_ragged(qkv, oracle, torch_gpu, L):
 
 
 def test_verify_T8_q8(qkv, oracle, torch_gpu):
-    """BASELINE config 4 shape (T = 8, causal among the 8, all q8), at a shorter context, seed 3."""
+    """The verify shape (T = 8, causal among the 8, all q8), at a shorter context, seed 3."""
     check_case(qkv, oracle, torch_gpu, "", 0, 3000, 8, seed=3)
 
 

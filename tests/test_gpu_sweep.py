@@ -1,0 +1,61 @@
+"""A seeded randomized sweep over the store and attention parameters: per case a random MK_KV spec (bits 4..8 per side,
+rotations), window, context length, T (capped to one 640-bucket as the reference's att_cap_T does), 1..3 sequences
+on a shared page pool with a shuffled page table.  Every stored row is compared bit for bit and every attention
+output within 2e-3 (max-abs relative) against the oracle."""
+import numpy as np
+import pytest
+
+from kvcase import HD, NH, NKV, check_rows, expected_attention, rel_err, synth_kv
+
+pytestmark = pytest.mark.gpu
+
+
+def random_spec(rng):
+    items = []
+    for side in "KV":
+        b = int(rng.integers(4, 9))
+        items.append(f"{side}*={b}{'r' if b < 8 and rng.random() < 0.5 else ''}")
+    return ",".join(items)
+
+
+@pytest.mark.parametrize("case", range(8))
+def test_random_case(qkv, oracle, torch_gpu, case):
+    torch = torch_gpu
+    rng = np.random.default_rng(1000 + case)
+    spec = random_spec(rng)
+    win = int(rng.choice([0, 256, 640, 2048]))
+    n_seq = int(rng.integers(1, 4))
+    page = 256
+    lens = [int(rng.integers(1, 4200)) for _ in range(n_seq)]
+    ctx = 4352
+    npg = ctx // page
+    T = int(rng.integers(1, 9))
+    T = min(T, min(lens))
+    T = min([qkv.cap_T(L - T, T) for L in lens] + [T])  # the T rows of every sequence stay inside one bucket
+    T = max(T, 1)
+    st = qkv.KVStore(spec, win=win, n_layers=1, n_seq=n_seq, ctx=ctx, page=page, n_pages=n_seq * npg)
+    perm = rng.permutation(n_seq * npg)
+    data = []
+    print(f"case {case}: spec={spec} win={win} lens={lens} T={T}", flush=True)
+    for s, L in enumerate(lens):
+        st.set_pages(s, perm[s * npg:(s + 1) * npg])
+        K, V = synth_kv(rng, L, 1, outliers=bool(rng.random() < 0.5))
+        k = torch.from_numpy(K).cuda()
+        v = torch.from_numpy(V).cuda()
+        st.append(s, 0, 1, 0, L, k.data_ptr(), v.data_ptr(), 0)
+        torch.cuda.synchronize()
+        check_rows(oracle, st, K, V, seq=s, ring_from=max(0, L - qkv.ring_rows(win)) if win else 0)
+        data.append((K, V))
+    Q = rng.standard_normal((1, n_seq, T, NH, HD)).astype(np.float32)
+    q = torch.from_numpy(Q).cuda()
+    o = torch.full_like(q, float("nan"))
+    st.attend(0, 1, list(range(n_seq)), lens, T, q.data_ptr(), o.data_ptr())
+    torch.cuda.synchronize()
+    out = o.cpu().numpy()
+    kb, vb, kr, vr = st.kbits[0], st.vbits[0], st.krot[0], st.vrot[0]
+    for s, L in enumerate(lens):
+        K, V = data[s]
+        ws = qkv.window_start(L, win)
+        ref = expected_attention(oracle, Q[0, s], K[:, 0], V[:, 0], T, kr, vr, kb, vb, ws, win > 0 and kb != 8, win > 0 and vb != 8)
+        assert rel_err(out[0, s], ref) <= 2e-3, (case, spec, win, L, T)
+    st.close()

@@ -590,7 +590,8 @@ static int prefill_impl(void * h, int seq, int layer0, int n_layers, int pos, in
             p.ws = window_start(p.L, s.win);
             p.R = GQA * Tp;
             p.nrb = (p.R + PF2_ROWS - 1) / PF2_ROWS;
-            p.nseg = (p.L + PF_SEG - 1) / PF_SEG;
+            p.seg = pf_seg(p.L);
+            p.nseg = (p.L + p.seg - 1) / p.seg;
             p.qs = qs;
             p.gs = gs;
             p.rope = qnw ? s.rope : nullptr;

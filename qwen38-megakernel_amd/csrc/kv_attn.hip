@@ -858,9 +858,10 @@ hipError_t launch_combine(const AttnArgs & a, hipStream_t st, hipEvent_t ev0, hi
 
 // ------------------------------------------------------------------------------------------------ prefill
 // Causal attention of one prefill piece (pk_attn8's exact form, prefill_attn.cuh:698-702; pieces and window
-// prefill_host.cu:606-615).  Keys are cut into absolute segments of PF_SEG positions; a row's partial for segment k is
-// one online softmax over the segment's tiles in order, and the combine folds the row's segments 0 .. pos / PF_SEG in
-// order: each output is a function of its position and the store only, whatever the chunking of the prefill.
+// prefill_host.cu:606-615).  Keys are cut into absolute segments of a.seg positions (a function of the row's bucket); a
+// row's partial for segment k is one online softmax over the segment's tiles in order, and the combine folds the row's
+// segments 0 .. pos / a.seg in order: each output is a function of its position and the store only, whatever the
+// chunking of the prefill.
 
 // 32 values of scale block b (dims 32 b .. 32 b + 31) of one staged row of B bits -> 16 fp16 pairs fp16_rn(d q), the
 // same values as the decode operands (kfrag)
@@ -963,9 +964,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const int g = bi % NKV, k = bi / NKV;
     const int r0 = PF2_ROWS * rb, rlast = min(a.R, r0 + PF2_ROWS) - 1;
     const int pmax = a.n0 + rlast / GQA;
-    const int c0 = k * PF_SEG;
+    const int c0 = k * a.seg;
     if (c0 > pmax) return;
-    const int c1 = min(c0 + PF_SEG, pmax + 1);
+    const int c1 = min(c0 + a.seg, pmax + 1);
     const int ntiles = (c1 - c0 + ATP - 1) / ATP;
     const unsigned lds0 = (unsigned) (size_t) (__attribute__((address_space(3))) uint8_t *) smem;
     _Float16 * const buf0 = reinterpret_cast<_Float16 *>(smem + PQ_STAGES);
@@ -1117,14 +1118,14 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     }
 }
 
-// One wave per (row, kv head) of a prefill piece: the row's segments 0 .. pos / PF_SEG folded in segment order
+// One wave per (row, kv head) of a prefill piece: the row's segments 0 .. pos / a.seg folded in segment order
 // (M' = max(M, m_k), O' = O e^(M - M') + O_k e^(m_k - M'), l likewise), y = O / l, then the output epilogue.
 __global__ __launch_bounds__(256) void k_prefill_combine(PrefillArgs a) {
     const int wid = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
     if (wid >= a.R * NKV) return;
     const int r = wid % a.R, g = wid / a.R;
     const int t = r / GQA, hh = r - GQA * t, pos = a.n0 + t;
-    const int nk = pos / PF_SEG + 1;
+    const int nk = pos / a.seg + 1;
     float M = -INFINITY, den = 0.f;
     float4 num = make_float4(0.f, 0.f, 0.f, 0.f);
     for (int k = 0; k < nk; k++) {

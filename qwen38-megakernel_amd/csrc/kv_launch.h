@@ -40,12 +40,13 @@ struct AttnArgs {
 };
 
 // one prefill piece of one layer: query rows r = 6 t + hh (token t = 0 .. Tp-1 at position n0 + t, query head
-// 6 g + hh of kv head g), keys in absolute segments of PF_SEG positions
+// 6 g + hh of kv head g), keys in absolute segments of `seg` positions (pf_seg of the piece's bucket)
 struct PrefillArgs {
     StoreLayout S;
     int layer, seq;
     int n0, Tp, L, ws; // first query position, rows' tokens, L = n0 + Tp (one 640-bucket), window start of the bucket
-    int R, nrb, nseg;  // 6 Tp rows per kv head, ceil(R / PF2_ROWS) row blocks, ceil(L / PF_SEG) key segments
+    int R, nrb, nseg;  // 6 Tp rows per kv head, ceil(R / PF2_ROWS) row blocks, ceil(L / seg) key segments
+    int seg;           // key positions per segment
     int krot, vrot;
     const float * q;   // [Tp][NH][qs]
     int qs;
@@ -60,7 +61,13 @@ struct PrefillArgs {
     float * part;      // [NKV][nseg][R][HD] per-segment partial outputs (unnormalised)
     float2 * ml;       // [NKV][nseg][R] (max in log2 units, sum)
 };
-constexpr int PF_SEG = 4096; // key positions per prefill segment (a multiple of 32)
+// key positions per prefill segment: 2,048 ceil(Lb / 32,768) with Lb = L rounded up to its 640-bucket, so at most 16
+// segments per row (the partials stay small at long contexts) and the same segments for every row of a bucket (every
+// row's result is a function of its position)
+inline int pf_seg(int L) {
+    const int lb = (L + ATT_BUCKET - 1) / ATT_BUCKET * ATT_BUCKET;
+    return 2048 * ((lb + 32767) / 32768);
+}
 constexpr int PF2_ROWS = 128; // query rows per prefill workgroup (32 per wave)
 
 // canonical segment length: 128 ceil(Lb / 16384) positions with Lb = L rounded up to a 640 bucket: a multiple of 4 tiles,

@@ -439,7 +439,7 @@ static int attend_impl(void * h, int layer0, int n_layers, int n_seq, const int 
         a.gs = gs;
         a.qnw = qnw;
         a.R = GQA * T;
-        a.RP = a.R <= 8 ? 8 : 16; // one 8-row group (T = 1), else batches of 16 rows
+        a.RP = a.R <= 8 ? 8 : a.R <= 16 ? 16 : 24; // T = 1: one 8-row group; T = 2: 16 rows; T >= 3: batches of 24 rows
         a.nseq = n_seq;
         int seg_total = 0;
         for (int i = 0; i < n_seq; i++) {

@@ -334,7 +334,7 @@ __device__ __forceinline__ void read_v(RawTile<KB, VB> & r, const uint8_t * st, 
 }
 
 // ------------------------------------------------------------------------------------------------ the tile
-// Query rows go in NP groups of 8 (NP = ceil(6 T / 8), rounded up to 1, 2, 3 or 6).  Both MFMA products use the 16
+// Query rows go in NP groups of 8 (NP = 1, 2 or 3: 8, 16 or 24 rows per pass).  Both MFMA products use the 16
 // columns as (row, e) pairs, row = 8 h + n / 2 of group h and e = n % 2:
 //   S^T = K Q^T   column n of Q^T is query row 8 h + n / 2 (each score is computed in lanes n and n ^ 1), so lane
 //                 (n, q) owns its row's scores at positions 4 q + e and 16 + 4 q + e (e = 0..3);
@@ -355,9 +355,13 @@ struct WaveState {
 // query rows in LDS: fp16 [RP][256] with 16-byte chunk c of row r stored at chunk c ^ (r % 16)
 __device__ __forceinline__ int qchunk(int r, int c) { return r * (HD / 8) + (c ^ (r & 15)); }
 
+// vst (optional): the tile's stage; the V operands are then read from it after the scores (raw.v unset on entry)
 template <int NP, int KB, int VB>
-__device__ __forceinline__ void compute_tile(WaveState<NP> & st, const half8 * sQ, int p0, const RawTile<KB, VB> & raw) {
-    const int lane = lane_id(), q = lane >> 4, n = lane & 15;
+__device__ __forceinline__ void compute_tile(WaveState<NP> & st, const half8 * sQ, int p0, RawTile<KB, VB> & raw,
+                                             const uint8_t * vst = nullptr) {
+    int lane = lane_id(); // opaque: lane-derived LDS addresses are recomputed per tile, not held across the loop
+    asm volatile("" : "+v"(lane));
+    const int q = lane >> 4, n = lane & 15;
     // ---- S^T = K Q^T, two 16-position subtiles
     f32x4 s[NP][2];
 #pragma unroll
@@ -439,6 +443,7 @@ __device__ __forceinline__ void compute_tile(WaveState<NP> & st, const half8 * s
 #pragma unroll
             for (int b = 0; b < 8; b++) st.acc[h][b] *= alpha[h];
     }
+    if (vst) read_v<KB, VB>(raw, vst, n, q);
     // ---- O += P V: block b = dims 16 m + 2 b, + 1 of the lane's V row m (nibble word b / 4, values 2 (b % 4), + 1)
     half2v dv[8];
 #pragma unroll
@@ -487,21 +492,25 @@ __device__ __forceinline__ void set_prio(int left) {
 }
 
 // ------------------------------------------------------------------------------------------------ the kernel
-// More than 16 query rows (T >= 3) run as batches of 16 rows: work item = (sequence, layer, kv head, segment, row
-// batch), batch-minor; each batch streams the segment's tiles again with the two-group kernel, so no kernel holds more
-// than two groups of accumulators, and every row sees the same slices, tile arithmetic and merge whatever T.  The
-// batches of a segment run side by side, so its second and third reads mostly hit the last-level cache.
+// More than 16 query rows (T >= 3) run as batches of 24 rows (one pass for T <= 4, two for T = 5..8): work item =
+// (sequence, layer, kv head, segment, row batch), batch-minor; each batch streams the segment's tiles again with the
+// three-group kernel (48 rows of accumulators in one wave spill), and every row sees the same slices, tile arithmetic
+// and merge whatever T.  The batches of a segment run side by side, so the second read mostly hits the last-level
+// cache.
 template <int NP, int KB, int VB>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NP == 1 ? 2 : 1, NP == 1 ? 2 : 1))) void k_attn(AttnArgs a) {
     constexpr int RP = 8 * NP; // query rows held (the padding rows are zero)
+    // NP >= 3: two stages per wave; the next tile streams into the other stage, and the V operands are read from the
+    // stage after the scores, so a wave never holds a whole raw tile in registers next to 24-48 rows of accumulators
+    constexpr int NST = NP >= 3 ? 2 : 1;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     // the wave index as a scalar: tile positions, page lookups and source selection stay scalar (SMEM loads, uniform
     // branches); vector loads there would need vmcnt waits that also drain the tile copies in flight
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63, n = lane & 15, q = lane >> 4;
     const StoreLayout & S = a.S;
     const unsigned lds0 = (unsigned) (size_t) (__attribute__((address_space(3))) uint8_t *) smem;
-    const unsigned st_lds = (unsigned) __builtin_amdgcn_readfirstlane(lds0 + wv * STAGE_BYTES);
-    half8 * const sQ = reinterpret_cast<half8 *>(smem + ATTN_LDS); // [RP][256] fp16, chunk-swizzled (qchunk)
+    const unsigned st_lds0 = (unsigned) __builtin_amdgcn_readfirstlane(lds0 + wv * NST * STAGE_BYTES);
+    half8 * const sQ = reinterpret_cast<half8 *>(smem + NST * ATTN_LDS); // [RP][256] fp16, chunk-swizzled (qchunk)
     for (int bitem = blockIdx.x; bitem < a.n_items; bitem += gridDim.x) {
         const int nb = a.n_items / a.n_base, item = bitem / nb, batch = bitem - item * nb, row0 = RP * batch;
         int si = 0;
@@ -522,10 +531,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NP == 1 ? 2
 
         auto issue = [&](int i) {
             const int p0 = c0 + ATP * (wv + AWAVES * i), nv = min(ATP, L - p0);
+            const unsigned st_lds = st_lds0 + (NST == 2 && (i & 1) ? STAGE_BYTES : 0);
             const bool ring = S.kvrc > 0 && p0 >= ws; // the window: q8 rows (ring, or the main store of q8 sides)
             const TileSrc t = tile_src<KB, VB>(S, SK, SV, seq, g, p0, ring0, ring);
-            if (ring) issue_tile<8, 8>(t, nv, st_lds, lane);
-            else issue_tile<KB, VB>(t, nv, st_lds, lane);
+            int ln = lane; // opaque: the per-lane chunk addresses are not hoisted out of the tile loop into registers
+            asm volatile("" : "+v"(ln));
+            if (ring) issue_tile<8, 8>(t, nv, st_lds, ln);
+            else issue_tile<KB, VB>(t, nv, st_lds, ln);
         };
 
         if (my > 0) issue(0);
@@ -557,27 +569,48 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NP == 1 ? 2
         }
         st.lim_min = L - T;
         __syncthreads(); // the query rows are complete
-        const uint8_t * const stp = smem + wv * STAGE_BYTES; // (derived from smem: LDS reads)
-        for (int i = 0; i < my; i++) {
+        const uint8_t * const stp0 = smem + wv * NST * STAGE_BYTES; // (derived from smem: LDS reads)
+        // the wave's window (ring) tiles are its last ones: i >= i_ring, p0 >= ws.  Two loops, one tile format each,
+        // keep a single tile body live per loop (one body holding both formats costs registers)
+        int i_ring = my;
+        if (S.kvrc > 0) {
+            const int d = ws - c0 - ATP * wv;
+            i_ring = d <= 0 ? 0 : min(my, (d + AWAVES * ATP - 1) / (AWAVES * ATP));
+        }
+        // operands into registers, then the stage is free and the next tile streams in during this one's math
+        int i = 0;
+        for (; i < i_ring; i++) {
             set_prio(my - i);
             vm_wait<0>(); // tile i has landed (the wave's only copies in flight)
-            const int p0 = c0 + ATP * (wv + AWAVES * i);
-            const bool ring = S.kvrc > 0 && p0 >= ws;
-            // operands into registers, then the stage is free and the next tile streams in during this one's math
-            if (ring) {
-                RawTile<8, 8> raw;
-                read_k<8, 8>(raw, stp, n, q);
-                read_v<8, 8>(raw, stp, n, q);
-                lds_drain();
+            RawTile<KB, VB> raw;
+            if constexpr (NST == 2) { // the other stage's reads were consumed by the last tile's math
+                const uint8_t * const stp = stp0 + (i & 1) * STAGE_BYTES;
                 if (i + 1 < my) issue(i + 1);
-                compute_tile<NP, 8, 8>(st, sQ, p0, raw);
-            } else {
-                RawTile<KB, VB> raw;
                 read_k<KB, VB>(raw, stp, n, q);
-                read_v<KB, VB>(raw, stp, n, q);
+                compute_tile<NP, KB, VB>(st, sQ, c0 + ATP * (wv + AWAVES * i), raw, stp);
+            } else {
+                read_k<KB, VB>(raw, stp0, n, q);
+                read_v<KB, VB>(raw, stp0, n, q);
                 lds_drain();
                 if (i + 1 < my) issue(i + 1);
-                compute_tile<NP, KB, VB>(st, sQ, p0, raw);
+                compute_tile<NP, KB, VB>(st, sQ, c0 + ATP * (wv + AWAVES * i), raw);
+            }
+        }
+        for (; i < my; i++) {
+            set_prio(my - i);
+            vm_wait<0>();
+            RawTile<8, 8> raw;
+            if constexpr (NST == 2) { // the other stage's reads were consumed by the last tile's math
+                const uint8_t * const stp = stp0 + (i & 1) * STAGE_BYTES;
+                if (i + 1 < my) issue(i + 1);
+                read_k<8, 8>(raw, stp, n, q);
+                compute_tile<NP, 8, 8>(st, sQ, c0 + ATP * (wv + AWAVES * i), raw, stp);
+            } else {
+                read_k<8, 8>(raw, stp0, n, q);
+                read_v<8, 8>(raw, stp0, n, q);
+                lds_drain();
+                if (i + 1 < my) issue(i + 1);
+                compute_tile<NP, 8, 8>(st, sQ, c0 + ATP * (wv + AWAVES * i), raw);
             }
         }
         // ---- merge the 4 waves in order: M = max m_w, O = sum e_w O_w, l = sum e_w l_w.  Per pass of 16 rows (two
@@ -1178,12 +1211,13 @@ hipError_t launch_attn(const AttnArgs & a, int kb, int vb, int max_blocks, hipSt
     const int np = a.RP / 8;
     if (np == 1) k = pick<1>(kb, vb);
     else if (np == 2) k = pick<2>(kb, vb);
+    else if (np == 3) k = pick<3>(kb, vb);
     if (!k) return hipErrorInvalidValue;
     static thread_local const void * configured[128];
     static thread_local int n_configured = 0;
     bool done = false;
     for (int i = 0; i < n_configured; i++) done |= configured[i] == (const void *) k;
-    const int lds = ATTN_LDS + a.RP * HD * 2;
+    const int lds = (np >= 3 ? 2 : 1) * ATTN_LDS + a.RP * HD * 2;
     if (!done) {
         const hipError_t e = hipFuncSetAttribute((const void *) k, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
         if (e != hipSuccess) return e;

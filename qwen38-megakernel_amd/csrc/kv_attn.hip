@@ -355,10 +355,20 @@ struct WaveState {
 // query rows in LDS: fp16 [RP][256] with 16-byte chunk c of row r stored at chunk c ^ (r % 16)
 __device__ __forceinline__ int qchunk(int r, int c) { return r * (HD / 8) + (c ^ (r & 15)); }
 
-// vst (optional): the tile's stage; the V operands are then read from it after the scores (raw.v unset on entry)
-template <int NP, int KB, int VB>
+template <int K, int V>
+struct Fmt {
+    static constexpr int kb = K, vb = V;
+};
+
+struct NoHook {
+    __device__ void operator()() const {}
+};
+
+// LATE_V: raw.v is unset on entry; the V operands are read from the stage vst after the scores, and after_v() (which
+// refills the stage) runs once they are in registers -- K and V are never live together next to 24 rows of state
+template <int NP, int KB, int VB, bool LATE_V = false, typename F = NoHook>
 __device__ __forceinline__ void compute_tile(WaveState<NP> & st, const half8 * sQ, int p0, RawTile<KB, VB> & raw,
-                                             const uint8_t * vst = nullptr) {
+                                             const uint8_t * vst = nullptr, F after_v = F()) {
     int lane = lane_id(); // opaque: lane-derived LDS addresses are recomputed per tile, not held across the loop
     asm volatile("" : "+v"(lane));
     const int q = lane >> 4, n = lane & 15;
@@ -443,7 +453,11 @@ __device__ __forceinline__ void compute_tile(WaveState<NP> & st, const half8 * s
 #pragma unroll
             for (int b = 0; b < 8; b++) st.acc[h][b] *= alpha[h];
     }
-    if (vst) read_v<KB, VB>(raw, vst, n, q);
+    if constexpr (LATE_V) {
+        read_v<KB, VB>(raw, vst, n, q);
+        lds_drain();
+        after_v();
+    }
     // ---- O += P V: block b = dims 16 m + 2 b, + 1 of the lane's V row m (nibble word b / 4, values 2 (b % 4), + 1)
     half2v dv[8];
 #pragma unroll
@@ -498,19 +512,19 @@ __device__ __forceinline__ void set_prio(int left) {
 // and merge whatever T.  The batches of a segment run side by side, so the second read mostly hits the last-level
 // cache.
 template <int NP, int KB, int VB>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NP == 1 ? 2 : 1, NP == 1 ? 2 : 1))) void k_attn(AttnArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_attn(AttnArgs a) {
     constexpr int RP = 8 * NP; // query rows held (the padding rows are zero)
-    // NP >= 3: two stages per wave; the next tile streams into the other stage, and the V operands are read from the
-    // stage after the scores, so a wave never holds a whole raw tile in registers next to 24-48 rows of accumulators
-    constexpr int NST = NP >= 3 ? 2 : 1;
+    // NP = 3: the V operands are read from the stage after the scores (the stage is refilled only then), so a wave
+    // never holds a whole raw tile in registers next to 24 rows of accumulators, and two workgroups fit a CU
+    constexpr bool LATE_V = NP >= 3;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     // the wave index as a scalar: tile positions, page lookups and source selection stay scalar (SMEM loads, uniform
     // branches); vector loads there would need vmcnt waits that also drain the tile copies in flight
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63, n = lane & 15, q = lane >> 4;
     const StoreLayout & S = a.S;
     const unsigned lds0 = (unsigned) (size_t) (__attribute__((address_space(3))) uint8_t *) smem;
-    const unsigned st_lds0 = (unsigned) __builtin_amdgcn_readfirstlane(lds0 + wv * NST * STAGE_BYTES);
-    half8 * const sQ = reinterpret_cast<half8 *>(smem + NST * ATTN_LDS); // [RP][256] fp16, chunk-swizzled (qchunk)
+    const unsigned st_lds = (unsigned) __builtin_amdgcn_readfirstlane(lds0 + wv * STAGE_BYTES);
+    half8 * const sQ = reinterpret_cast<half8 *>(smem + ATTN_LDS); // [RP][256] fp16, chunk-swizzled (qchunk)
     for (int bitem = blockIdx.x; bitem < a.n_items; bitem += gridDim.x) {
         const int nb = a.n_items / a.n_base, item = bitem / nb, batch = bitem - item * nb, row0 = RP * batch;
         int si = 0;
@@ -531,7 +545,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NP == 1 ? 2
 
         auto issue = [&](int i) {
             const int p0 = c0 + ATP * (wv + AWAVES * i), nv = min(ATP, L - p0);
-            const unsigned st_lds = st_lds0 + (NST == 2 && (i & 1) ? STAGE_BYTES : 0);
             const bool ring = S.kvrc > 0 && p0 >= ws; // the window: q8 rows (ring, or the main store of q8 sides)
             const TileSrc t = tile_src<KB, VB>(S, SK, SV, seq, g, p0, ring0, ring);
             int ln = lane; // opaque: the per-lane chunk addresses are not hoisted out of the tile loop into registers
@@ -569,7 +582,26 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NP == 1 ? 2
         }
         st.lim_min = L - T;
         __syncthreads(); // the query rows are complete
-        const uint8_t * const stp0 = smem + wv * NST * STAGE_BYTES; // (derived from smem: LDS reads)
+        const uint8_t * const stp = smem + wv * STAGE_BYTES; // (derived from smem: LDS reads)
+        // one tile: operands into registers, then the stage is free and the next tile streams in during the math
+        auto step = [&](auto fmt, int i) {
+            constexpr int K2 = decltype(fmt)::kb, V2 = decltype(fmt)::vb;
+            set_prio(my - i);
+            vm_wait<0>(); // tile i has landed (the wave's only copies in flight)
+            RawTile<K2, V2> raw;
+            read_k<K2, V2>(raw, stp, n, q);
+            const int p0 = c0 + ATP * (wv + AWAVES * i);
+            if constexpr (LATE_V) {
+                compute_tile<NP, K2, V2, true>(st, sQ, p0, raw, stp, [&]() {
+                    if (i + 1 < my) issue(i + 1);
+                });
+            } else {
+                read_v<K2, V2>(raw, stp, n, q);
+                lds_drain();
+                if (i + 1 < my) issue(i + 1);
+                compute_tile<NP, K2, V2>(st, sQ, p0, raw);
+            }
+        };
         // the wave's window (ring) tiles are its last ones: i >= i_ring, p0 >= ws.  Two loops, one tile format each,
         // keep a single tile body live per loop (one body holding both formats costs registers)
         int i_ring = my;
@@ -577,42 +609,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NP == 1 ? 2
             const int d = ws - c0 - ATP * wv;
             i_ring = d <= 0 ? 0 : min(my, (d + AWAVES * ATP - 1) / (AWAVES * ATP));
         }
-        // operands into registers, then the stage is free and the next tile streams in during this one's math
         int i = 0;
-        for (; i < i_ring; i++) {
-            set_prio(my - i);
-            vm_wait<0>(); // tile i has landed (the wave's only copies in flight)
-            RawTile<KB, VB> raw;
-            if constexpr (NST == 2) { // the other stage's reads were consumed by the last tile's math
-                const uint8_t * const stp = stp0 + (i & 1) * STAGE_BYTES;
-                if (i + 1 < my) issue(i + 1);
-                read_k<KB, VB>(raw, stp, n, q);
-                compute_tile<NP, KB, VB>(st, sQ, c0 + ATP * (wv + AWAVES * i), raw, stp);
-            } else {
-                read_k<KB, VB>(raw, stp0, n, q);
-                read_v<KB, VB>(raw, stp0, n, q);
-                lds_drain();
-                if (i + 1 < my) issue(i + 1);
-                compute_tile<NP, KB, VB>(st, sQ, c0 + ATP * (wv + AWAVES * i), raw);
-            }
-        }
-        for (; i < my; i++) {
-            set_prio(my - i);
-            vm_wait<0>();
-            RawTile<8, 8> raw;
-            if constexpr (NST == 2) { // the other stage's reads were consumed by the last tile's math
-                const uint8_t * const stp = stp0 + (i & 1) * STAGE_BYTES;
-                if (i + 1 < my) issue(i + 1);
-                read_k<8, 8>(raw, stp, n, q);
-                compute_tile<NP, 8, 8>(st, sQ, c0 + ATP * (wv + AWAVES * i), raw, stp);
-            } else {
-                read_k<8, 8>(raw, stp0, n, q);
-                read_v<8, 8>(raw, stp0, n, q);
-                lds_drain();
-                if (i + 1 < my) issue(i + 1);
-                compute_tile<NP, 8, 8>(st, sQ, c0 + ATP * (wv + AWAVES * i), raw);
-            }
-        }
+        for (; i < i_ring; i++) step(Fmt<KB, VB>(), i);
+        for (; i < my; i++) step(Fmt<8, 8>(), i);
         // ---- merge the 4 waves in order: M = max m_w, O = sum e_w O_w, l = sum e_w l_w.  Per pass of 16 rows (two
         // groups) every wave writes its scaled O rows to its own LDS buffer (the stages are free), then each thread
         // adds the 4 buffers in wave order.
@@ -1217,7 +1216,7 @@ hipError_t launch_attn(const AttnArgs & a, int kb, int vb, int max_blocks, hipSt
     static thread_local int n_configured = 0;
     bool done = false;
     for (int i = 0; i < n_configured; i++) done |= configured[i] == (const void *) k;
-    const int lds = (np >= 3 ? 2 : 1) * ATTN_LDS + a.RP * HD * 2;
+    const int lds = ATTN_LDS + a.RP * HD * 2;
     if (!done) {
         const hipError_t e = hipFuncSetAttribute((const void *) k, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
         if (e != hipSuccess) return e;

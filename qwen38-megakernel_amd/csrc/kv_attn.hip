@@ -616,9 +616,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         // groups) every wave writes its scaled O rows to its own LDS buffer (the stages are free), then each thread
         // adds the 4 buffers in wave order.
         constexpr int OLD = HD + 4;                                                   // row stride (floats) of a buffer
-        float * const s_m = reinterpret_cast<float *>(smem + AWAVES * 16 * OLD * 4); // [AWAVES][RP]
+        constexpr int MR = NP == 1 ? 8 : 16;                                          // rows per wave buffer
+        float * const s_m = reinterpret_cast<float *>(smem + AWAVES * MR * OLD * 4); // [AWAVES][RP]
         float * const s_l = s_m + AWAVES * RP;                                        // [AWAVES][RP]
-        static_assert(AWAVES * 16 * OLD * 4 + 2 * AWAVES * 48 * 4 <= ATTN_LDS, "merge buffers inside the stages");
+        static_assert(AWAVES * MR * OLD * 4 + 2 * AWAVES * 48 * 4 <= ATTN_LDS, "merge buffers inside the stages");
         __syncthreads(); // every wave is done with its stage
         if (q == 0 && !(n & 1)) {
 #pragma unroll
@@ -639,7 +640,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                     const int row = 8 * h + (n >> 1);
                     const float M = fmaxf(fmaxf(s_m[row], s_m[RP + row]), fmaxf(s_m[2 * RP + row], s_m[3 * RP + row]));
                     const float e = st.m[h] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(st.m[h] - M);
-                    float * o = reinterpret_cast<float *>(smem) + (wv * 16 + 8 * hh + (n >> 1)) * OLD + 64 * q + (n & 1);
+                    float * o = reinterpret_cast<float *>(smem) + (wv * MR + 8 * hh + (n >> 1)) * OLD + 64 * q + (n & 1);
 #pragma unroll
                     for (int b = 0; b < 8; b++)
 #pragma unroll
@@ -654,7 +655,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                 float4 y = *reinterpret_cast<const float4 *>(src);
 #pragma unroll
                 for (int w = 1; w < AWAVES; w++) {
-                    const float4 z = *reinterpret_cast<const float4 *>(src + w * 16 * OLD);
+                    const float4 z = *reinterpret_cast<const float4 *>(src + w * MR * OLD);
                     y.x += z.x;
                     y.y += z.y;
                     y.z += z.z;

@@ -73,11 +73,13 @@ def test_rotated_v_and_mixed_layers(qkv, oracle, torch_gpu):
     check_case(qkv, oracle, torch_gpu, "K0=4r,V0=7r,K1=8,V1=5,K2=6,V2=8r", 640, 2500, 2, nl=3, seed=5)
 
 
-def test_t_invariance(qkv, oracle, torch_gpu):
-    """Token t of a T-row call equals a 1-row call at context n+t+1 (bitwise; bench/dattn_bench.cu:1140-1160)."""
+@pytest.mark.parametrize("T", [2, 3, 5, 8])
+def test_t_invariance(qkv, oracle, torch_gpu, T):
+    """Token t of a T-row call equals a 1-row call at context n+t+1 (bitwise; bench/dattn_bench.cu:1140-1160).
+    T = 2 runs the 16-row kernel, T = 3 one 24-row batch, T = 5 a full and a ragged 24-row batch, T = 8 two."""
     torch = torch_gpu
-    L, T = 3190, 8
-    st, out, (K, V, Q) = check_case(qkv, oracle, torch, "K*=5r,V*=6", 1024, L, T, seed=9)
+    L = 3190
+    st, out, (K, V, Q) = check_case(qkv, oracle, torch, "K*=5r,V*=6", 1024, L, T, seed=9 + T)
     for t in range(T):
         o1 = run_attend(torch, st, Q[:, :, t:t + 1], [0], [L - T + t + 1], 1)
         assert np.array_equal(o1[:, :, 0], out[:, :, t]), t

@@ -141,10 +141,16 @@ def bench_cfg1(torch, qkv, steps, warmup):
     gen_fill(torch, st, 0, L, 1, seed=0, outliers=False)
     q = torch.randn(1, 1, 1, NH, HD, device="cuda")
     out = torch.empty_like(q)
-    t = timed(torch, lambda: st.attend(0, 1, [0], [L], 1, q.data_ptr(), out.data_ptr()), steps * 5, warmup)
+    fn = lambda: st.attend(0, 1, [0], [L], 1, q.data_ptr(), out.data_ptr())
+    t = timed(torch, fn, steps * 5, warmup)
+    prof = profiled(torch, st, fn, steps * 5)
+    attn = prof["attn_ms"] / prof["calls"] * 1e-3
+    comb = prof["combine_ms"] / prof["calls"] * 1e-3
     b = NKV * L * 2 * BYTES[8]
     return {"L": L, "call_s": t, "positions_per_s": L / t, "gbps": b / t / 1e9,
-            "note": "8.9 MB per call: resident in the 256 MB last-level cache across calls"}
+            "attn_kernel_avg_s": attn, "combine_avg_s": comb, "attn_kernel_gbps": b / attn / 1e9,
+            "note": "8.9 MB per call: resident in the 256 MB last-level cache across calls; the kernel times come from "
+                    "a second pass with per-launch events, which lengthen short launches"}
 
 
 def bench_cfg2(torch, qkv, nsteps=512):

@@ -1,7 +1,9 @@
 """A seeded randomized sweep over the store and attention parameters: per case a random MK_KV spec (bits 4..8 per side,
 rotations), window, context length, T (capped to one 640-bucket as the reference's att_cap_T does), 1..3 sequences
 on a shared page pool with a shuffled page table.  Every stored row is compared bit for bit and every attention
-output within 2e-3 (max-abs relative) against the oracle."""
+output within 2e-3 (max-abs relative) against the oracle.  QKV_SWEEP_CASES sets the number of cases (default 8)."""
+import os
+
 import numpy as np
 import pytest
 
@@ -18,7 +20,7 @@ def random_spec(rng):
     return ",".join(items)
 
 
-@pytest.mark.parametrize("case", range(8))
+@pytest.mark.parametrize("case", range(int(os.environ.get("QKV_SWEEP_CASES", "8"))))
 def test_random_case(qkv, oracle, torch_gpu, case):
     torch = torch_gpu
     rng = np.random.default_rng(1000 + case)

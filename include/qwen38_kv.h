@@ -162,7 +162,10 @@ int mk_kv_write_rows(void * h, int seq, int layer, int w, int g, int p0, int n, 
 long long mk_kv_ring_snapshot(void * h, int seq, void * dst, long long cap);
 int mk_kv_ring_restore(void * h, int seq, int pos, const void * src, long long bytes);
 
-/* Knobs: "max_blocks" caps the attention grid (0: one workgroup per work item); results never depend on it. */
+/* Knobs: "max_blocks" caps the attention grid (0: one workgroup per work item); "occupancy" sets the decode
+ * workgroups per CU for one-token calls on packed formats of at most 11 bits per K + V value: 0 (default) = three
+ * when a launch has more work items than two per CU hold, else two; 2 or 3 = always that.  Results never depend on
+ * either. */
 int mk_kv_config(void * h, const char * key, long long value);
 
 /* Kernel timing with HIP events on the launch stream (the reference's MK_PROFILE per-phase means, engine.cu:382-506).

@@ -114,6 +114,7 @@ struct Store {
     void * ml = nullptr;
     size_t ml_bytes = 0;
     int max_blocks = 0;
+    int occupancy = 0; // decode workgroups per CU: 0 = by launch size, 2 or 3 (launch_attn)
     // RoPE table of the Q/K prep calls: [rope_rows][32] (cos, sin), the caller's or the store's own text table
     const float2 * rope = nullptr;
     int rope_rows = 0;
@@ -506,7 +507,7 @@ static int attend_impl(void * h, int layer0, int n_layers, int n_seq, const int 
         auto ev = [&](int i, size_t g) { return es && ((i % 2 == 0 && g == 0) || (i % 2 == 1 && g + 1 == ng)) ? es->e[i] : nullptr; };
         for (size_t g = 0; g < ng; g++) {
             const AttnArgs & b = groups[g];
-            HCK(launch_attn(b, s.S.side[b.layer0][0].bits, s.S.side[b.layer0][1].bits, s.max_blocks, st, ev(0, g), ev(1, g)));
+            HCK(launch_attn(b, s.S.side[b.layer0][0].bits, s.S.side[b.layer0][1].bits, s.max_blocks, s.occupancy, st, ev(0, g), ev(1, g)));
         }
         for (size_t g = 0; g < ng; g++) HCK(launch_combine(groups[g], st, ev(2, g), ev(3, g)));
         return 0;
@@ -834,6 +835,11 @@ int mk_kv_config(void * h, const char * key, long long value) {
         if (!strcmp(key, "max_blocks")) {
             if (value < 0) throw std::runtime_error("max_blocks must be >= 0");
             s.max_blocks = (int) value;
+            return 0;
+        }
+        if (!strcmp(key, "occupancy")) {
+            if (value != 0 && value != 2 && value != 3) throw std::runtime_error("occupancy must be 0 (by launch size), 2 or 3");
+            s.occupancy = (int) value;
             return 0;
         }
         throw std::runtime_error(std::string("unknown knob ") + key);

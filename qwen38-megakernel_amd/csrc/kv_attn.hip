@@ -307,6 +307,30 @@ __device__ __forceinline__ int issue_tile(const TileSrc & t, int nv, unsigned ld
     return KB + VB + 1;
 }
 
+// a q8 tile through a stage smaller than one (three workgroups per CU): part 0 = the K rows at 0 and every scale at
+// 8 KiB, part 1 = the V rows at 0 once the K operands are in registers; partial tiles clamp as issue_tile does
+template <int PART>
+__device__ __forceinline__ void issue_q8_part(const TileSrc & t, int nv, unsigned lds, int lane) {
+    const uint8_t * const src = PART == 0 ? t.k : t.v;
+    if (nv == ATP) {
+        const unsigned off = 16 * lane;
+#pragma unroll
+        for (int j = 0; j < 8; j++) dma16s(src + 1024 * j, off, lds + 1024 * j);
+    } else {
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            int c = j * 64 + lane;
+            const int r = c / 16;
+            if (r >= nv) c = (nv - 1) * 16 + (c - r * 16);
+            dma16(src + 16 * c, lds + 1024 * j);
+        }
+    }
+    if constexpr (PART == 0) {
+        const int r = min(lane & 31, nv - 1);
+        dma16(lane < 32 ? static_cast<const void *>(t.ks + 8 * r) : static_cast<const void *>(t.vs + 8 * r), lds + 8192);
+    }
+}
+
 template <int KB, int VB>
 struct RawTile {
     KSub<KB> k0, k1; // subtile rows n, 16 + n
@@ -316,21 +340,25 @@ struct RawTile {
 // the lane's operands of a staged tile into registers (row n = l % 16, quarter q = l / 16): the K subtiles, then,
 // separately, the V positions (read after the scores, so the K and V registers are never live together)
 template <int KB, int VB>
-__device__ __forceinline__ void read_k(RawTile<KB, VB> & r, const uint8_t * st, int n, int q) {
-    const uint8_t * kr = st;
-    const uint16_t * ksc = reinterpret_cast<const uint16_t *>(st + 1024 * (KB + VB));
+__device__ __forceinline__ void read_k(RawTile<KB, VB> & r, const uint8_t * kr, const uint16_t * ksc, int n, int q) {
     load_ksub<KB>(r.k0, kr + n * 32 * KB, ksc + n * 8, q);
     load_ksub<KB>(r.k1, kr + (16 + n) * 32 * KB, ksc + (16 + n) * 8, q);
 }
 template <int KB, int VB>
-__device__ __forceinline__ void read_v(RawTile<KB, VB> & r, const uint8_t * st, int n, int q) {
-    const uint8_t * vr = st + 1024 * KB;
-    const uint16_t * vsc = reinterpret_cast<const uint16_t *>(st + 1024 * (KB + VB)) + 8 * ATP;
+__device__ __forceinline__ void read_k(RawTile<KB, VB> & r, const uint8_t * st, int n, int q) {
+    read_k<KB, VB>(r, st, reinterpret_cast<const uint16_t *>(st + 1024 * (KB + VB)), n, q);
+}
+template <int KB, int VB>
+__device__ __forceinline__ void read_v(RawTile<KB, VB> & r, const uint8_t * vr, const uint16_t * vsc, int n, int q) {
 #pragma unroll
     for (int j = 0; j < 8; j++) {
         const int row = j < 4 ? 4 * q + j : 16 + 4 * q + j - 4;
         load_vpos<VB>(r.v, j, vr + row * 32 * VB, vsc + row * 8, n);
     }
+}
+template <int KB, int VB>
+__device__ __forceinline__ void read_v(RawTile<KB, VB> & r, const uint8_t * st, int n, int q) {
+    read_v<KB, VB>(r, st + 1024 * KB, reinterpret_cast<const uint16_t *>(st + 1024 * (KB + VB)) + 8 * ATP, n, q);
 }
 
 // ------------------------------------------------------------------------------------------------ the tile
@@ -361,14 +389,15 @@ struct Fmt {
 };
 
 struct NoHook {
-    __device__ void operator()() const {}
+    template <typename... A>
+    __device__ void operator()(A &&...) const {}
 };
 
-// LATE_V: raw.v is unset on entry; the V operands are read from the stage vst after the scores, and after_v() (which
-// refills the stage) runs once they are in registers -- K and V are never live together next to 24 rows of state
-template <int NP, int KB, int VB, bool LATE_V = false, typename F = NoHook>
+// LATE_V: raw.v is unset on entry; load_v(raw, n, q) reads the V operands from the stage after the scores, and after_v()
+// (which refills the stage) runs once they are in registers -- K and V are never live together next to the state
+template <int NP, int KB, int VB, bool LATE_V = false, typename FV = NoHook, typename FA = NoHook>
 __device__ __forceinline__ void compute_tile(WaveState<NP> & st, const half8 * sQ, int p0, RawTile<KB, VB> & raw,
-                                             const uint8_t * vst = nullptr, F after_v = F()) {
+                                             FV load_v = FV(), FA after_v = FA()) {
     int lane = lane_id(); // opaque: lane-derived LDS addresses are recomputed per tile, not held across the loop
     asm volatile("" : "+v"(lane));
     const int q = lane >> 4, n = lane & 15;
@@ -454,7 +483,7 @@ __device__ __forceinline__ void compute_tile(WaveState<NP> & st, const half8 * s
             for (int b = 0; b < 8; b++) st.acc[h][b] *= alpha[h];
     }
     if constexpr (LATE_V) {
-        read_v<KB, VB>(raw, vst, n, q);
+        load_v(raw, n, q); // (the tile's lane indices: recomputed per tile)
         lds_drain();
         after_v();
     }
@@ -511,20 +540,25 @@ __device__ __forceinline__ void set_prio(int left) {
 // three-group kernel (48 rows of accumulators in one wave spill), and every row sees the same slices, tile arithmetic
 // and merge whatever T.  The batches of a segment run side by side, so the second read mostly hits the last-level
 // cache.
-template <int NP, int KB, int VB>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_attn(AttnArgs a) {
+// SMALL (one 8-row group, KB + VB <= 11): three workgroups per CU for launches with many work items.  The stages hold
+// one packed tile (32 (KB + VB) + 1 KiB); a q8 window tile goes through in two halves (issue_q8_part); the V operands
+// are read after the scores (168 registers).  Same slices and arithmetic: bitwise the same partials.
+template <int NP, int KB, int VB, bool SMALL = false>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SMALL ? 3 : 2, SMALL ? 3 : 2))) void k_attn(AttnArgs a) {
+    static_assert(!SMALL || (NP == 1 && KB + VB <= 11), "small stages: one row group, packed tiles of at most 11 KiB");
     constexpr int RP = 8 * NP; // query rows held (the padding rows are zero)
+    constexpr int SB = SMALL ? 1024 * (KB + VB) + 1024 : STAGE_BYTES, SLDS = AWAVES * SB; // stage bytes, all stages
     // NP = 3: the V operands are read from the stage after the scores (the stage is refilled only then), so a wave
     // never holds a whole raw tile in registers next to 24 rows of accumulators, and two workgroups fit a CU
-    constexpr bool LATE_V = NP >= 3;
+    constexpr bool LATE_V = NP >= 3 || SMALL;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     // the wave index as a scalar: tile positions, page lookups and source selection stay scalar (SMEM loads, uniform
     // branches); vector loads there would need vmcnt waits that also drain the tile copies in flight
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63, n = lane & 15, q = lane >> 4;
     const StoreLayout & S = a.S;
     const unsigned lds0 = (unsigned) (size_t) (__attribute__((address_space(3))) uint8_t *) smem;
-    const unsigned st_lds = (unsigned) __builtin_amdgcn_readfirstlane(lds0 + wv * STAGE_BYTES);
-    half8 * const sQ = reinterpret_cast<half8 *>(smem + ATTN_LDS); // [RP][256] fp16, chunk-swizzled (qchunk)
+    const unsigned st_lds = (unsigned) __builtin_amdgcn_readfirstlane(lds0 + wv * SB);
+    half8 * const sQ = reinterpret_cast<half8 *>(smem + SLDS); // [RP][256] fp16, chunk-swizzled (qchunk)
     for (int bitem = blockIdx.x; bitem < a.n_items; bitem += gridDim.x) {
         const int nb = a.n_items / a.n_base, item = bitem / nb, batch = bitem - item * nb, row0 = RP * batch;
         int si = 0;
@@ -549,8 +583,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             const TileSrc t = tile_src<KB, VB>(S, SK, SV, seq, g, p0, ring0, ring);
             int ln = lane; // opaque: the per-lane chunk addresses are not hoisted out of the tile loop into registers
             asm volatile("" : "+v"(ln));
-            if (ring) issue_tile<8, 8>(t, nv, st_lds, ln);
-            else issue_tile<KB, VB>(t, nv, st_lds, ln);
+            if (ring) {
+                if constexpr (SMALL) issue_q8_part<0>(t, nv, st_lds, ln);
+                else issue_tile<8, 8>(t, nv, st_lds, ln);
+            } else {
+                issue_tile<KB, VB>(t, nv, st_lds, ln);
+            }
         };
 
         if (my > 0) issue(0);
@@ -582,20 +620,42 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         }
         st.lim_min = L - T;
         __syncthreads(); // the query rows are complete
-        const uint8_t * const stp = smem + wv * STAGE_BYTES; // (derived from smem: LDS reads)
+        const uint8_t * const stp = smem + wv * SB; // (derived from smem: LDS reads)
         // one tile: operands into registers, then the stage is free and the next tile streams in during the math
         auto step = [&](auto fmt, int i) {
             constexpr int K2 = decltype(fmt)::kb, V2 = decltype(fmt)::vb;
             set_prio(my - i);
             vm_wait<0>(); // tile i has landed (the wave's only copies in flight)
             RawTile<K2, V2> raw;
-            read_k<K2, V2>(raw, stp, n, q);
             const int p0 = c0 + ATP * (wv + AWAVES * i);
-            if constexpr (LATE_V) {
-                compute_tile<NP, K2, V2, true>(st, sQ, p0, raw, stp, [&]() {
-                    if (i + 1 < my) issue(i + 1);
-                });
+            if constexpr (SMALL && K2 == 8 && V2 == 8) { // a q8 window tile in two halves
+                const uint16_t * const sc = reinterpret_cast<const uint16_t *>(stp + 8192);
+                read_k<8, 8>(raw, stp, sc, n, q);
+                lds_drain(); // the K rows are in registers: the V half may overwrite them
+                {
+                    const TileSrc t = tile_src<KB, VB>(S, SK, SV, seq, g, p0, ring0, true);
+                    int ln = lane;
+                    asm volatile("" : "+v"(ln));
+                    issue_q8_part<1>(t, min(ATP, L - p0), st_lds, ln);
+                }
+                compute_tile<NP, 8, 8, true>(
+                    st, sQ, p0, raw,
+                    [&](RawTile<8, 8> & r, int tn, int tq) {
+                        vm_wait<0>(); // the V half has landed
+                        read_v<8, 8>(r, stp, sc + 8 * ATP, tn, tq);
+                    },
+                    [&]() {
+                        if (i + 1 < my) issue(i + 1);
+                    });
+            } else if constexpr (LATE_V) {
+                read_k<K2, V2>(raw, stp, n, q);
+                compute_tile<NP, K2, V2, true>(
+                    st, sQ, p0, raw, [&](RawTile<K2, V2> & r, int tn, int tq) { read_v<K2, V2>(r, stp, tn, tq); },
+                    [&]() {
+                        if (i + 1 < my) issue(i + 1);
+                    });
             } else {
+                read_k<K2, V2>(raw, stp, n, q);
                 read_v<K2, V2>(raw, stp, n, q);
                 lds_drain();
                 if (i + 1 < my) issue(i + 1);
@@ -619,7 +679,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         constexpr int MR = NP == 1 ? 8 : 16;                                          // rows per wave buffer
         float * const s_m = reinterpret_cast<float *>(smem + AWAVES * MR * OLD * 4); // [AWAVES][RP]
         float * const s_l = s_m + AWAVES * RP;                                        // [AWAVES][RP]
-        static_assert(AWAVES * MR * OLD * 4 + 2 * AWAVES * 48 * 4 <= ATTN_LDS, "merge buffers inside the stages");
+        static_assert(AWAVES * MR * OLD * 4 + 2 * AWAVES * RP * 4 <= SLDS, "merge buffers inside the stages");
         __syncthreads(); // every wave is done with its stage
         if (q == 0 && !(n & 1)) {
 #pragma unroll
@@ -1206,10 +1266,51 @@ static AttnKernel pick(int kb, int vb) {
 #undef QKV_VB
 }
 
-hipError_t launch_attn(const AttnArgs & a, int kb, int vb, int max_blocks, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {
+template <int KB, int VB>
+static AttnKernel small_or_null() {
+    if constexpr (KB + VB <= 11) return k_attn<1, KB, VB, true>;
+    else return nullptr;
+}
+
+static AttnKernel pick_small(int kb, int vb) {
+#define QKV_VB(K)                                                                                                      \
+    switch (vb) {                                                                                                      \
+    case 4: return small_or_null<K, 4>();                                                                              \
+    case 5: return small_or_null<K, 5>();                                                                              \
+    case 6: return small_or_null<K, 6>();                                                                              \
+    case 7: return small_or_null<K, 7>();                                                                              \
+    default: return nullptr;                                                                                           \
+    }
+    switch (kb) {
+    case 4: QKV_VB(4)
+    case 5: QKV_VB(5)
+    case 6: QKV_VB(6)
+    case 7: QKV_VB(7)
+    default: return nullptr;
+    }
+#undef QKV_VB
+}
+
+// CUs of the current device (cached per thread and device)
+static int device_cus() {
+    static thread_local int dev_cached = -1, cus = 0;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 256;
+    if (dev != dev_cached) {
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+        dev_cached = dev;
+    }
+    return cus;
+}
+
+hipError_t launch_attn(const AttnArgs & a, int kb, int vb, int max_blocks, int occ, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {
     AttnKernel k = nullptr;
     const int np = a.RP / 8;
-    if (np == 1) k = pick<1>(kb, vb);
+    // three workgroups per CU (small stages) when one 8-row group of a packed format of at most 11 KiB per tile has
+    // more work items than two per CU hold (occ 0), or always (occ 3); occ 2 keeps two
+    const bool small = np == 1 && kb + vb <= 11 && (occ == 3 || (occ == 0 && a.n_items > 2 * device_cus()));
+    if (small) k = pick_small(kb, vb);
+    else if (np == 1) k = pick<1>(kb, vb);
     else if (np == 2) k = pick<2>(kb, vb);
     else if (np == 3) k = pick<3>(kb, vb);
     if (!k) return hipErrorInvalidValue;
@@ -1217,7 +1318,7 @@ hipError_t launch_attn(const AttnArgs & a, int kb, int vb, int max_blocks, hipSt
     static thread_local int n_configured = 0;
     bool done = false;
     for (int i = 0; i < n_configured; i++) done |= configured[i] == (const void *) k;
-    const int lds = ATTN_LDS + a.RP * HD * 2;
+    const int lds = (small ? AWAVES * (1024 * (kb + vb) + 1024) : ATTN_LDS) + a.RP * HD * 2;
     if (!done) {
         const hipError_t e = hipFuncSetAttribute((const void *) k, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
         if (e != hipSuccess) return e;

@@ -89,7 +89,9 @@ hipError_t launch_append(const StoreLayout & S, int seq, int layer0, int nl, int
                          hipStream_t st, hipEvent_t ev0 = nullptr, hipEvent_t ev1 = nullptr, const float * knw = nullptr,
                          const float2 * rope = nullptr);
 hipError_t launch_ring_refill(const StoreLayout & S, int seq, int nl, int p0, int p1, hipStream_t st);
-hipError_t launch_attn(const AttnArgs & a, int kb, int vb, int max_blocks, hipStream_t st, hipEvent_t ev0 = nullptr,
+// occ: workgroups per CU for one 8-row group of packed formats up to 11 KiB per tile: 0 = three when the launch has more
+// work items than two per CU hold, else two; 2 = two; 3 = three
+hipError_t launch_attn(const AttnArgs & a, int kb, int vb, int max_blocks, int occ, hipStream_t st, hipEvent_t ev0 = nullptr,
                        hipEvent_t ev1 = nullptr);
 hipError_t launch_combine(const AttnArgs & a, hipStream_t st, hipEvent_t ev0 = nullptr, hipEvent_t ev1 = nullptr);
 hipError_t launch_prefill(const PrefillArgs & a, int kb, int vb, hipStream_t st, hipEvent_t ev0 = nullptr, hipEvent_t ev1 = nullptr);

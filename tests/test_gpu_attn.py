@@ -96,6 +96,19 @@ def test_grid_invariance(qkv, oracle, torch_gpu):
     assert np.array_equal(run_attend(torch, st, Q, [0], [7000], 1), out)
 
 
+@pytest.mark.parametrize("spec,win,L", [("K*=5r,V*=6", 2048, 7001), ("K*=4,V*=7r", 640, 5000), ("K*=4r,V*=4", 256, 3333),
+                                        ("K*=6,V*=5r", 2048, 4100)])
+def test_occupancy_invariance(qkv, oracle, torch_gpu, spec, win, L):
+    """Three workgroups per CU (stages of one packed tile; q8 window tiles copied in two halves) give the same bits as
+    two, with window tiles, a partial last tile and two layers in the launch; occupancy 0 picks by launch size."""
+    torch = torch_gpu
+    st, out, (K, V, Q) = check_case(qkv, oracle, torch, spec, win, L, 1, nl=2, seed=11, outliers=True)
+    for occ in (3, 2, 0, 3):
+        st.config("occupancy", occ)
+        assert np.array_equal(run_attend(torch, st, Q, [0], [L], 1), out), occ
+    st.config("occupancy", 0)
+
+
 def test_ring_on_q8_sides_changes_nothing(qkv, oracle, torch_gpu):
     """MK_KV_WIN_ALL (loader.cu:1487-1490): q8 rings on q8 sides give byte-identical outputs."""
     torch = torch_gpu

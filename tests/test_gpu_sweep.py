@@ -1,6 +1,6 @@
 """A seeded randomized sweep over the store and attention parameters: per case a random MK_KV spec (bits 4..8 per side,
 rotations), window, context length, T (capped to one 640-bucket as the reference's att_cap_T does), 1..3 sequences
-on a shared page pool with a shuffled page table.  Every stored row is compared bit for bit and every attention
+on a shared page pool with a shuffled page table, and the decode occupancy knob.  Every stored row is compared bit for bit and every attention
 output within 2e-3 (max-abs relative) against the oracle.  QKV_SWEEP_CASES sets the number of cases (default 8)."""
 import os
 
@@ -36,9 +36,11 @@ def test_random_case(qkv, oracle, torch_gpu, case):
     T = min([qkv.cap_T(L - T, T) for L in lens] + [T])  # the T rows of every sequence stay inside one bucket
     T = max(T, 1)
     st = qkv.KVStore(spec, win=win, n_layers=1, n_seq=n_seq, ctx=ctx, page=page, n_pages=n_seq * npg)
+    occ = int(np.random.default_rng(5000 + case).choice([0, 3]))  # 3: small stages where the format allows
+    st.config("occupancy", occ)
     perm = rng.permutation(n_seq * npg)
     data = []
-    print(f"case {case}: spec={spec} win={win} lens={lens} T={T}", flush=True)
+    print(f"case {case}: spec={spec} win={win} lens={lens} T={T} occupancy={occ}", flush=True)
     for s, L in enumerate(lens):
         st.set_pages(s, perm[s * npg:(s + 1) * npg])
         K, V = synth_kv(rng, L, 1, outliers=bool(rng.random() < 0.5))

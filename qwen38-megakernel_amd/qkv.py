@@ -240,4 +240,6 @@ class KVStore:
         return dict(zip(("calls", "attn_ms", "combine_ms", "append_ms"), list(out)))
 
     def config(self, key, value):
+        """Knobs that never change results: "max_blocks" (attention grid cap, 0 = none) and "occupancy" (decode
+        workgroups per CU for one-token calls on small packed formats: 0 = by launch size, 2 or 3)."""
         _check(lib().mk_kv_config(self.h, key.encode(), value))

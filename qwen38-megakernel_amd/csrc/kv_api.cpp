@@ -40,42 +40,65 @@ struct Spec {
     int kb[SLOTS], vb[SLOTS], kr[SLOTS], vr[SLOTS];
 };
 
-// MK_KV grammar (loader.cu:1329-1365): <K|V|*><slot>=<4..8>[r], comma separated; slot empty or * = all slots
-void parse_spec(const char * spec, int n_layers, Spec & s) {
-    for (int i = 0; i < SLOTS; i++) {
-        s.kb[i] = s.vb[i] = 8;
-        s.kr[i] = s.vr[i] = 0;
+// MK_KV grammar (loader.cu:1329-1365): comma-separated items <side><slot>=<bits>[r], side K, V or * (both), slot a
+// number (strtol syntax), empty or * (all slots), bits 4..8, r = stored Walsh-Hadamard rotated; empty items are
+// skipped and later items override earlier ones.  The accepted strings and the three messages are the reference's.
+struct SpecItem {
+    bool side[2]; // applies to K, V
+    int slot;     // -1: every slot
+    int bits;
+    int rot;
+};
+
+SpecItem parse_item(const std::string & tok, int n_layers) {
+    const size_t eq = tok.find('=');
+    const char side = tok[0];
+    if (eq == std::string::npos || eq == 0 || (side != 'K' && side != 'V' && side != '*'))
+        throw std::runtime_error("MK_KV: bad item " + tok);
+    SpecItem it{};
+    it.side[0] = side != 'V';
+    it.side[1] = side != 'K';
+    // the format: one digit 4..8, optionally followed by 'r'
+    const char * fmt = tok.c_str() + eq + 1;
+    const size_t flen = tok.size() - eq - 1;
+    const bool digit_ok = flen >= 1 && fmt[0] >= '4' && fmt[0] <= '8';
+    const bool suffix_ok = flen == 1 || (flen == 2 && fmt[1] == 'r');
+    if (!digit_ok || !suffix_ok) throw std::runtime_error("MK_KV: expected 4..8 or 4r..8r in " + tok);
+    it.bits = fmt[0] - '0';
+    it.rot = flen == 2;
+    // the slot text between the side letter and '='
+    const std::string slot_txt(tok, 1, eq - 1);
+    it.slot = -1;
+    if (!slot_txt.empty() && slot_txt != "*") {
+        char * stop = nullptr;
+        const long v = strtol(slot_txt.c_str(), &stop, 10);
+        if (*stop != '\0' || v < 0 || v >= n_layers)
+            throw std::runtime_error("MK_KV: bad slot in " + tok + " (0.." + std::to_string(n_layers - 1) + " or *)");
+        it.slot = (int) v;
     }
-    if (!spec || !spec[0]) return;
-    const std::string str = spec;
-    size_t i = 0;
-    while (i < str.size()) {
-        size_t j = str.find(',', i);
-        if (j == std::string::npos) j = str.size();
-        const std::string tok = str.substr(i, j - i);
-        i = j + 1;
-        if (tok.empty()) continue;
-        const size_t e = tok.find('=');
-        if (e == std::string::npos || e == 0 || !strchr("KV*", tok[0])) throw std::runtime_error("MK_KV: bad item " + tok);
-        const std::string sl = tok.substr(1, e - 1), md = tok.substr(e + 1);
-        if (md.empty() || md.size() > 2 || md[0] < '4' || md[0] > '8' || (md.size() == 2 && md[1] != 'r'))
-            throw std::runtime_error("MK_KV: expected 4..8 or 4r..8r in " + tok);
-        const bool rot = md.size() == 2;
-        const bool all = sl.empty() || sl == "*";
-        long slot = -1;
-        if (!all) {
-            char * end = nullptr;
-            slot = strtol(sl.c_str(), &end, 10);
-            if (*end || slot < 0 || slot >= n_layers)
-                throw std::runtime_error("MK_KV: bad slot in " + tok + " (0.." + std::to_string(n_layers - 1) + " or *)");
+    return it;
+}
+
+void parse_spec(const char * spec, int n_layers, Spec & s) {
+    std::fill(s.kb, s.kb + SLOTS, 8);
+    std::fill(s.vb, s.vb + SLOTS, 8);
+    std::fill(s.kr, s.kr + SLOTS, 0);
+    std::fill(s.vr, s.vr + SLOTS, 0);
+    if (!spec) return;
+    const char * p = spec;
+    for (;;) {
+        const char * comma = strchr(p, ',');
+        const std::string tok = comma ? std::string(p, comma) : std::string(p);
+        if (!tok.empty()) {
+            const SpecItem it = parse_item(tok, n_layers);
+            const int lo = it.slot < 0 ? 0 : it.slot, hi = it.slot < 0 ? n_layers : it.slot + 1;
+            for (int k = lo; k < hi; k++) {
+                if (it.side[0]) s.kb[k] = it.bits, s.kr[k] = it.rot;
+                if (it.side[1]) s.vb[k] = it.bits, s.vr[k] = it.rot;
+            }
         }
-        for (int w = 0; w < 2; w++)
-            if (tok[0] == '*' || tok[0] == "KV"[w])
-                for (int k = 0; k < n_layers; k++)
-                    if (all || k == slot) {
-                        (w ? s.vb : s.kb)[k] = md[0] - '0';
-                        (w ? s.vr : s.kr)[k] = rot;
-                    }
+        if (!comma) break;
+        p = comma + 1;
     }
 }
 
@@ -201,6 +224,9 @@ template <class F> int guarded(F f) {
         return f();
     } catch (const std::exception & e) {
         g_err = e.what();
+        return -1;
+    } catch (...) {
+        g_err = "unknown exception";
         return -1;
     }
 }
@@ -378,6 +404,10 @@ void * mk_kv_new(const char * kv_spec, int win, int win_all, int n_layers, int n
         g_err = e.what();
         delete s;
         return nullptr;
+    } catch (...) {
+        g_err = "unknown exception";
+        delete s;
+        return nullptr;
     }
 }
 
@@ -449,6 +479,14 @@ static int attend_impl(void * h, int layer0, int n_layers, int n_seq, const int 
             if (L < T || L > s.ctx) throw std::runtime_error("context length " + std::to_string(L) + " outside T .. ctx");
             if ((L - T + ATT_BUCKET_) / ATT_BUCKET_ != (L - 1 + ATT_BUCKET_) / ATT_BUCKET_)
                 throw std::runtime_error("the T rows straddle a 640-position bucket (cap T with mk_kv_cap_T)");
+            if (L > s.n[seqs[i]])
+                throw std::runtime_error("context length " + std::to_string(L) + " beyond the " + std::to_string(s.n[seqs[i]]) +
+                                         " positions stored for sequence " + std::to_string(seqs[i]));
+            // the window rows ws .. L-1 are read from the ring, which holds the newest kvrc rows written: rows older
+            // than top - kvrc have been overwritten by later appends (rewind first to attend there)
+            if (s.ring_bytes && s.top[seqs[i]] - s.kvrc > window_start(L, s.win))
+                throw std::runtime_error("context length " + std::to_string(L) + ": its window rows were overwritten in the ring by " +
+                                         "positions up to " + std::to_string(s.top[seqs[i]] - 1) + " (rewind first)");
             SeqDesc & d = a.sd[i];
             d.seq = seqs[i];
             d.L = L;
@@ -686,10 +724,13 @@ int mk_kv_read_rows(void * h, int seq, int layer, int w, int g, int p0, int n, i
         HCK(hipDeviceSynchronize());
         if (ring) {
             if (!sd.ring) throw std::runtime_error("this side has no window ring");
-            for (int i = 0; i < n; i++) {
-                const size_t r = (size_t) (seq * NKV + g) * s.kvrc + (p0 + i) % s.kvrc;
-                if (vals) HCK(hipMemcpy(static_cast<uint8_t *>(vals) + (size_t) i * HD, sd.ring + r * HD, HD, hipMemcpyDeviceToHost));
-                if (scales) HCK(hipMemcpy(scales + (size_t) i * 8, sd.rsc + r * 8, 16, hipMemcpyDeviceToHost));
+            for (int i = 0; i < n;) { // runs of consecutive ring rows (a run ends where the ring wraps)
+                const int slot = (p0 + i) % s.kvrc, cnt = std::min(n - i, s.kvrc - slot);
+                const size_t r = (size_t) (seq * NKV + g) * s.kvrc + slot;
+                if (vals)
+                    HCK(hipMemcpy(static_cast<uint8_t *>(vals) + (size_t) i * HD, sd.ring + r * HD, (size_t) cnt * HD, hipMemcpyDeviceToHost));
+                if (scales) HCK(hipMemcpy(scales + (size_t) i * 8, sd.rsc + r * 8, (size_t) cnt * 16, hipMemcpyDeviceToHost));
+                i += cnt;
             }
             return HD;
         }

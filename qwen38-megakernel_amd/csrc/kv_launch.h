@@ -20,7 +20,7 @@ struct AttnArgs {
     StoreLayout S;
     int layer0;          // first slot of the launch
     int nl;              // layers in the launch (all with the same K/V bits)
-    int T, R, RP;        // query tokens, query rows per kv head (6 T), rows per batch: 8 (R <= 8) or 16
+    int T, R, RP;        // query tokens, query rows per kv head (6 T), rows per batch: 8 (R <= 8), 16 (R <= 16), else 24
     int nseq;
     int n_base;          // (sequence, layer, kv head, segment) work items
     int n_items;         // n_base * ceil(R / RP): every item once per row batch (batch-minor)

@@ -76,7 +76,9 @@ __global__ __launch_bounds__(256) void k_append(StoreLayout S, int seq, int laye
         }
     }
     if ((lane & 7) == 0) sd.scs[row * 8 + (lane >> 3)] = sc;
-    if (sd.ring) {
+    // ring copy: only for the newest kvrc positions of the call (p >= pos + T - kvrc); an older one shares its ring
+    // row with a newer position of the same launch and is evicted by it anyway, and writing both would race
+    if (sd.ring && p >= pos + T - S.kvrc) {
         uint16_t rs;
         const unsigned word = quant_q8(v, rs);
         const size_t rr = ring_row(S, seq, g, p);

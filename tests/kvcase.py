@@ -58,16 +58,24 @@ def expected_kv(oracle, X, rot, bits, ws, has_ring):
 
 def expected_attention(oracle, Q, Kl, Vl, T, krot, vrot, kbits, vbits, ws, kring, vring):
     """Q [T][24][256], Kl/Vl [L][4][256] of one layer/sequence -> out [T][24][256] (fp64 exact attention on the
-    fp16 operands; V un-rotated by the FWHT when V is stored rotated)."""
+    fp16 operands; V un-rotated by the FWHT when V is stored rotated).  The 4 kv heads run on host threads (the
+    oracle's C calls release the GIL)."""
+    from concurrent.futures import ThreadPoolExecutor
+
     out = np.zeros((T, NH, HD), np.float32)
-    for g in range(NKV):
+    R = GQA * T
+
+    def head(g):
         K = expected_kv(oracle, Kl[:, g], krot, kbits, ws, kring)
         V = expected_kv(oracle, Vl[:, g], vrot, vbits, ws, vring)
-        R = GQA * T
         q = np.zeros((R, HD), np.float32)
         for r in range(R):
             q[r] = oracle.q_prep(Q[r % T, GQA * g + r // T], krot)
-        y = oracle.attn_exact(q, K, V, T)
+        return oracle.attn_exact(q, K, V, T)
+
+    with ThreadPoolExecutor(NKV) as ex:
+        ys = list(ex.map(head, range(NKV)))
+    for g, y in enumerate(ys):
         for r in range(R):
             v = y[r]
             if vrot:

@@ -165,3 +165,28 @@ def test_attend_errors(qkv, torch_gpu):
         st.config("occupancy", 1)
     with pytest.raises(qkv.KVError, match="unknown knob"):
         st.config("no_such_knob", 0)
+
+
+def test_attend_rejects_unstored_and_evicted_rows(qkv, torch_gpu):
+    """A context past the stored rows, or one whose window rows later appends have overwritten in the ring, is
+    refused through the C ABI (mk_last_error); after a rewind to that length the call runs."""
+    torch = torch_gpu
+    rng = np.random.default_rng(17)
+    K, V = synth_kv(rng, 5000, 1)
+    st = qkv.KVStore("K*=5r,V*=6", win=640, n_layers=1, ctx=6000)
+    append_all(torch, st, 0, K, V)
+    q = torch.zeros(1, 1, 1, NH, HD, device="cuda")
+    out = torch.empty_like(q)
+    with pytest.raises(qkv.KVError, match="beyond the 5000 positions stored"):
+        st.attend(0, 1, [0], [5001], 1, q.data_ptr(), out.data_ptr())
+    with pytest.raises(qkv.KVError, match="overwritten"):
+        st.attend(0, 1, [0], [1000], 1, q.data_ptr(), out.data_ptr())
+    st.attend(0, 1, [0], [5000], 1, q.data_ptr(), out.data_ptr())
+    st.rewind(0, 1000)
+    st.attend(0, 1, [0], [1000], 1, q.data_ptr(), out.data_ptr())
+    torch.cuda.synchronize()
+    # a store without rings keeps every row: any stored length may be attended
+    flat = qkv.KVStore("", n_layers=1, ctx=6000)
+    append_all(torch, flat, 0, K, V)
+    flat.attend(0, 1, [0], [1000], 1, q.data_ptr(), out.data_ptr())
+    torch.cuda.synchronize()

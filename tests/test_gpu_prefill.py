@@ -60,7 +60,8 @@ def test_prefill_parity_and_chunking(qkv, oracle, torch_gpu, spec, win):
 
 
 def test_prefill_two_segments_then_decode(qkv, oracle, torch_gpu):
-    """A context past one 8192-position key segment (the combine folds two), then a decode step on the same store."""
+    """A 9,000-position context over five 2,048-position key segments (the combine folds up to five), then a decode step
+    on the same store."""
     torch = torch_gpu
     rng = np.random.default_rng(42)
     P, nl, win, spec = 9000, 1, 2048, "K*=5r,V*=6"

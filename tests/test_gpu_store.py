@@ -54,6 +54,19 @@ def test_ring_eviction(qkv, oracle, torch_gpu):
     check_rows(oracle, st, K, V, ring_from=T - 1312)
 
 
+def test_one_call_longer_than_the_ring(qkv, oracle, torch_gpu):
+    """One append of about 3 ring lengths: positions p and p + kvrc of the same launch share a ring row, and only the
+    newest kvrc positions may write it; the ring must hold exactly the last kvrc rows, whatever the dispatch order."""
+    torch = torch_gpu
+    rng = np.random.default_rng(16)
+    kvrc = qkv.ring_rows(512)
+    T = 3 * kvrc + 77
+    K, V = synth_kv(rng, T, 2, outliers=True)
+    st = qkv.KVStore("K*=5r,V0=6,V1=8", win=512, win_all=1, n_layers=2, ctx=T)
+    append_all(torch, st, 0, K, V)
+    check_rows(oracle, st, K, V, ring_from=T - kvrc)
+
+
 def test_paged_gathers_and_digest(qkv, oracle, torch_gpu):
     torch = torch_gpu
     rng = np.random.default_rng(13)

@@ -41,6 +41,12 @@ def test_parse_spec(qkv):
     assert kb == vb == [8] * 4 and kr == vr == [0] * 4
     kb, vb, kr, vr = qkv.parse_spec("*=4,K2=7r,V=6r", 4)   # later items override; empty slot = all
     assert kb == [4, 4, 7, 4] and vb == [6] * 4 and kr == [0, 0, 1, 0] and vr == [1] * 4
+    kb, vb, kr, vr = qkv.parse_spec(",,V1=7,,K+1=4r,", 3)   # empty items skipped; the slot is strtol syntax
+    assert kb == [8, 4, 8] and vb == [8, 7, 8] and kr == [0, 1, 0] and vr == [0] * 3
+    for bad, msg in [("K1=5=6", "expected 4..8"), ("K1=", "expected 4..8"), ("Kx=5", "bad slot"), ("K-1=5", "bad slot"),
+                     ("K3=5", "bad slot")]:
+        with pytest.raises(qkv.KVError, match=msg):
+            qkv.parse_spec(bad, 3)
     for bad, msg in [("X=5", "bad item"), ("K=9", "expected 4..8"), ("K99=5", "bad slot"), ("K*=5x", "expected"),
                      ("K1", "bad item"), ("=5", "bad item")]:
         with pytest.raises(qkv.KVError, match=msg):

@@ -7,7 +7,8 @@
  * message in the thread-local mk_last_error(); no exception crosses the ABI; caller-owned output buffers with a cap,
  * and cap 0 / NULL returns the count needed.  Device pointers are HIP device addresses already resident in HBM;
  * `stream` is a hipStream_t (NULL: the default stream).  One handle is not thread-safe: calls on it are serialised by
- * the caller, as with the reference's engine.
+ * the caller, as with the reference's engine.  The attend and prefill calls of one handle share its split-K workspace:
+ * issue them on one stream (or order the streams between calls), or their partials overwrite each other.
  *
  * Shapes: NKV = 4 kv heads, NH = 24 query heads (GQA 6), head dim 256, up to 17 attention slots (layers), up to 8
  * query tokens per attend call, up to 8 sequences per attend call.
@@ -65,6 +66,19 @@ int mk_kv_append(void * h, int seq, int layer0, int n_layers, int pos, int T, co
  */
 int mk_kv_attend(void * h, int layer0, int n_layers, int n_seq, const int * seqs, const int * lens, int T, const float * q, float * out,
                  void * stream);
+
+/*
+ * mk_kv_attend that allocates nothing: no hipMalloc / hipFree, no host heap.  No counterpart in the reference; for
+ * callers that cannot allocate (code under HIP graph capture, tight serving loops).  The segment partials go to a
+ * 64 MiB device array the library holds on each GPU it runs on (looked up on the first call on a device, which must be
+ * the store's device); a call whose partials need more fails with -1 and a message.  The partials take 1,032 bytes per
+ * (query row, split-K segment), at most 128 segments per kv head: 16 layers of one sequence at T = 1, or 2 layers at
+ * T = 8, fit at any context.  Every call on a GPU
+ * shares that GPU's array: calls that overlap on one GPU (several streams, threads or stores) race.  Nothing in it needs
+ * clearing: each call writes every partial it reads.  Same arguments, outputs and bits as mk_kv_attend.
+ */
+int mk_kv_attend_noalloc(void * h, int layer0, int n_layers, int n_seq, const int * seqs, const int * lens, int T, const float * q,
+                         float * out, void * stream);
 
 /*
  * mk_kv_attend followed by the combine epilogue (qwen38_mk.cu:4686-4688): out = y / (1 + exp(-gate)) with gate a

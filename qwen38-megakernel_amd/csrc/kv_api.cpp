@@ -8,6 +8,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <mutex>
 #include <cmath>
 #include <cstdint>
 #include <cstdlib>
@@ -123,6 +124,7 @@ uint64_t dg_hash(const void * p, size_t nb, uint64_t h = 0xcbf29ce484222325ULL) 
 }
 
 struct Store {
+    int dev = 0; // the HIP device the store's memory lives on
     int n_layers = 0, n_seq = 0, ctx = 0, page = 0, n_pages = 0, pt_stride = 0, win = 0, kvrc = 0, win_all = 0;
     Spec spec{};
     StoreLayout S{};
@@ -323,6 +325,26 @@ static void use_default_rope(Store & s) {
     s.rope_rows = s.ctx;
 }
 
+// The workspace of mk_kv_attend_noalloc: a file-scope device array (each GPU the library runs on holds its own copy
+// for the life of the process).  Host code never passes the array's name to a kernel: the name is a host-side stand-in,
+// so the device address is looked up once per device (hipGetSymbolAddress, with that device current) and kept.
+static constexpr size_t NOALLOC_SCRATCH_BYTES = 64ull << 20;
+static __device__ __align__(256) unsigned char scratch[NOALLOC_SCRATCH_BYTES];
+
+static void * noalloc_scratch(int dev) {
+    static std::mutex mu;
+    static void * addr[64] = {};
+    if (dev < 0 || dev >= 64) throw std::runtime_error("device index out of range for the allocation-free call");
+    std::lock_guard<std::mutex> lk(mu);
+    if (!addr[dev]) {
+        void * p = nullptr;
+        HCK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        if (!p) throw std::runtime_error("hipGetSymbolAddress returned no address for the workspace array");
+        addr[dev] = p;
+    }
+    return addr[dev];
+}
+
 extern "C" {
 
 const char * mk_last_error(void) { return g_err.c_str(); }
@@ -358,6 +380,7 @@ void * mk_kv_new(const char * kv_spec, int win, int win_all, int n_layers, int n
         if (win < 0) throw std::runtime_error("negative window");
         if (page < 0 || page % ATP_) throw std::runtime_error("page must be a multiple of 32 (0: contiguous)");
         s = new Store();
+        HCK(hipGetDevice(&s->dev));
         s->n_layers = n_layers;
         s->n_seq = n_seq;
         s->ctx = ctx;
@@ -450,9 +473,11 @@ static int append_impl(void * h, int seq, int layer0, int n_layers, int pos, int
 }
 
 // qs / gs: row strides (floats) of q and gate; qnw: q-norm weights (the Q prep) or null
+// ws (optional): a caller-provided workspace of ws_bytes for the segment partials, used instead of the store's own
+// (grown on demand) so that the call allocates nothing
 static int attend_impl(void * h, int layer0, int n_layers, int n_seq, const int * seqs, const int * lens, int T, const float * q,
                        int qs, const float * qnw, const float * gate, int gs, float * out, int8_t * q32a, int8_t * q32b, uint16_t * q32m,
-                       void * stream) {
+                       void * stream, void * ws = nullptr, size_t ws_bytes = 0) {
     return guarded([&] {
         Store & s = *as_store(h);
         if ((q32a != nullptr) != (q32b != nullptr) || (q32a != nullptr) != (q32m != nullptr))
@@ -506,11 +531,25 @@ static int attend_impl(void * h, int layer0, int n_layers, int n_seq, const int 
             a.vrot |= (unsigned) s.spec.vr[l] << l;
         }
         const size_t max_items = (size_t) n_layers * NKV * seg_total;
-        s.grow(s.part, s.part_bytes, max_items * a.R * HD * sizeof(float));
-        s.grow(s.ml, s.ml_bytes, max_items * a.R * sizeof(float2));
+        const size_t part_need = (max_items * a.R * HD * sizeof(float) + 255) / 256 * 256, ml_need = max_items * a.R * sizeof(float2);
+        float * part_base;
+        float2 * ml_base;
+        if (ws) {
+            if (part_need + ml_need > ws_bytes)
+                throw std::runtime_error("the call needs " + std::to_string(part_need + ml_need) + " bytes of attention workspace, more than the " +
+                                         std::to_string(ws_bytes) + " available to an allocation-free call");
+            part_base = static_cast<float *>(ws);
+            ml_base = reinterpret_cast<float2 *>(static_cast<char *>(ws) + part_need);
+        } else {
+            s.grow(s.part, s.part_bytes, part_need);
+            s.grow(s.ml, s.ml_bytes, ml_need);
+            part_base = static_cast<float *>(s.part);
+            ml_base = static_cast<float2 *>(s.ml);
+        }
         Store::EvSet * es = prof_set(s, 1);
         size_t item_base = 0;
-        std::vector<AttnArgs> groups;
+        AttnArgs groups[MAX_LAYERS]; // at most one launch per layer (no host allocation on this path)
+        size_t ng = 0;
         for (int l = 0; l < n_layers;) { // consecutive layers with the same K/V bits share one launch
             const int kb = s.S.side[layer0 + l][0].bits, vb = s.S.side[layer0 + l][1].bits;
             int e = l + 1;
@@ -534,14 +573,13 @@ static int attend_impl(void * h, int layer0, int n_layers, int n_seq, const int 
                 b.q32b = q32b + (size_t) l * n_seq * T * 192 * 16;
                 b.q32m = q32m + (size_t) l * n_seq * T * 192 * 4;
             }
-            b.part = static_cast<float *>(s.part) + item_base * a.R * HD;
-            b.ml = static_cast<float2 *>(s.ml) + item_base * a.R;
+            b.part = part_base + item_base * a.R * HD;
+            b.ml = ml_base + item_base * a.R;
             item_base += (size_t) item;
-            groups.push_back(b);
+            groups[ng++] = b;
             l = e;
         }
         // profiling: the first launch records the start event, the last the end event (kernel timestamps)
-        const size_t ng = groups.size();
         auto ev = [&](int i, size_t g) { return es && ((i % 2 == 0 && g == 0) || (i % 2 == 1 && g + 1 == ng)) ? es->e[i] : nullptr; };
         for (size_t g = 0; g < ng; g++) {
             const AttnArgs & b = groups[g];
@@ -568,6 +606,23 @@ int mk_kv_append_prep(void * h, int seq, int layer0, int n_layers, int pos, int 
 int mk_kv_attend(void * h, int layer0, int n_layers, int n_seq, const int * seqs, const int * lens, int T, const float * q, float * out,
                  void * stream) {
     return attend_impl(h, layer0, n_layers, n_seq, seqs, lens, T, q, HD, nullptr, nullptr, HD, out, nullptr, nullptr, nullptr, stream);
+}
+
+int mk_kv_attend_noalloc(void * h, int layer0, int n_layers, int n_seq, const int * seqs, const int * lens, int T, const float * q,
+                         float * out, void * stream) {
+    void * ws = nullptr;
+    const int r = guarded([&] {
+        const Store & s = *as_store(h);
+        int dev = -1;
+        HCK(hipGetDevice(&dev));
+        if (dev != s.dev)
+            throw std::runtime_error("the current device (" + std::to_string(dev) + ") is not the store's (" + std::to_string(s.dev) + ")");
+        ws = noalloc_scratch(dev);
+        return 0;
+    });
+    if (r < 0) return r;
+    return attend_impl(h, layer0, n_layers, n_seq, seqs, lens, T, q, HD, nullptr, nullptr, HD, out, nullptr, nullptr, nullptr, stream, ws,
+                       NOALLOC_SCRATCH_BYTES);
 }
 
 int mk_kv_attend_gated(void * h, int layer0, int n_layers, int n_seq, const int * seqs, const int * lens, int T, const float * q,

@@ -27,6 +27,7 @@ SIGNATURES = {
     "mk_kv_set_pages": (_c_int, [_c_vp, _c_int, _P_int, _c_int]),
     "mk_kv_append": (_c_int, [_c_vp, _c_int, _c_int, _c_int, _c_int, _c_int, _c_vp, _c_vp, _c_int, _c_vp]),
     "mk_kv_attend": (_c_int, [_c_vp, _c_int, _c_int, _c_int, _P_int, _P_int, _c_int, _c_vp, _c_vp, _c_vp]),
+    "mk_kv_attend_noalloc": (_c_int, [_c_vp, _c_int, _c_int, _c_int, _P_int, _P_int, _c_int, _c_vp, _c_vp, _c_vp]),
     "mk_kv_attend_gated": (_c_int, [_c_vp, _c_int, _c_int, _c_int, _P_int, _P_int, _c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _P_u16,
                                     _c_vp]),
     "mk_kv_set_rope": (_c_int, [_c_vp, _c_vp, _c_int]),
@@ -148,6 +149,13 @@ class KVStore:
         s = (ctypes.c_int * n)(*seqs)
         l = (ctypes.c_int * n)(*lens)
         _check(lib().mk_kv_attend(self.h, layer0, n_layers, n, s, l, T, q_ptr, out_ptr, stream))
+
+    def attend_noalloc(self, layer0, n_layers, seqs, lens, T, q_ptr, out_ptr, stream=0):
+        """attend with the partials in the library's per-device array (mk_kv_attend_noalloc): allocates nothing."""
+        n = len(seqs)
+        s = (ctypes.c_int * n)(*seqs)
+        l = (ctypes.c_int * n)(*lens)
+        _check(lib().mk_kv_attend_noalloc(self.h, layer0, n_layers, n, s, l, T, q_ptr, out_ptr, stream))
 
     def attend_gated(self, layer0, n_layers, seqs, lens, T, q_ptr, gate_ptr, out_ptr, q32a=0, q32b=0, q32meta=0, stream=0):
         """attend + the output gate (+ the int8 o_proj units when q32a / q32b / q32meta are device pointers)."""

@@ -500,6 +500,8 @@ static int attend_impl(void * h, int layer0, int n_layers, int n_seq, const int 
         int seg_total = 0;
         for (int i = 0; i < n_seq; i++) {
             check_seq(s, seqs[i]);
+            for (int j = 0; j < i; j++)
+                if (seqs[j] == seqs[i]) throw std::runtime_error("sequence " + std::to_string(seqs[i]) + " listed twice in one attend call");
             const int L = lens[i];
             if (L < T || L > s.ctx) throw std::runtime_error("context length " + std::to_string(L) + " outside T .. ctx");
             if ((L - T + ATT_BUCKET_) / ATT_BUCKET_ != (L - 1 + ATT_BUCKET_) / ATT_BUCKET_)

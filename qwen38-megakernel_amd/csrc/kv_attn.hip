@@ -28,13 +28,20 @@ namespace qkv {
 constexpr float LOG2E = 1.4426950408889634f;
 constexpr unsigned C64 = 0x64646464u;
 
-// main-store row of (seq, g, p) for wave-uniform arguments: the integer division runs on the vector unit, so the page
-// index is made scalar, and the table is read through the constant address space: a scalar load waits on lgkmcnt
-// only, never on the tile copies in flight
-__device__ __forceinline__ size_t attn_main_row(const StoreLayout & S, int seq, int g, int p) {
+// The page table is read through the constant address space (no kernel writes it during a launch): a scalar load,
+// which waits on lgkmcnt only, never on the tile copies in flight.  Its latency under a full HBM stream is of the order
+// of a tile's, so the tile loops look a tile's page up one step ahead (page_of), before they wait for the current tile.
+typedef const __attribute__((address_space(4))) int * const_int_p;
+
+// physical page of the logical page holding position p (wave-uniform) of sequence seq
+__device__ __forceinline__ int page_of(const StoreLayout & S, int seq, int p) {
     const int lp = __builtin_amdgcn_readfirstlane(p / S.page);
-    typedef const __attribute__((address_space(4))) int * const_int_p; // no kernel writes the table during a launch
-    const int phys = ((const_int_p) S.ptab)[seq * S.pt_stride + lp];
+    return ((const_int_p) S.ptab)[seq * S.pt_stride + lp];
+}
+
+// main-store row of (g, p) in physical page phys (the page of p)
+__device__ __forceinline__ size_t attn_main_row(const StoreLayout & S, int g, int p, int phys) {
+    const int lp = __builtin_amdgcn_readfirstlane(p / S.page);
     return (size_t) (g * S.n_pages + phys) * S.page + (p - lp * S.page);
 }
 
@@ -250,12 +257,13 @@ struct TileSrc {
 // the source rows of the 32 positions from p0 (wave-uniform) of (seq, kv head g): window tiles (ring) are q8 rows
 // from the ring of sides that have one, else from the main store (q8 sides); other tiles are main-store rows of
 // KB / VB bits.  ring0 = the first ring row of (seq, g).
+// phys: the physical page of p0 (page_of), looked up by the caller
 template <int KB, int VB>
-__device__ __forceinline__ TileSrc tile_src(const StoreLayout & S, const SideLayout & SK, const SideLayout & SV, int seq, int g, int p0,
+__device__ __forceinline__ TileSrc tile_src(const StoreLayout & S, const SideLayout & SK, const SideLayout & SV, int g, int p0, int phys,
                                            size_t ring0, bool ring) {
     TileSrc t;
     size_t mr = 0;
-    if (!ring || !SK.ring || !SV.ring) mr = attn_main_row(S, seq, g, p0);
+    if (!ring || !SK.ring || !SV.ring) mr = attn_main_row(S, g, p0, phys);
     const size_t rr = ring ? ring0 + __builtin_amdgcn_readfirstlane(p0 % max(S.kvrc, 1)) : 0;
     if (ring && SK.ring) {
         t.k = reinterpret_cast<const uint8_t *>(SK.ring) + rr * HD;
@@ -378,6 +386,9 @@ struct WaveState {
     float m[NP], l[NP];
     int lim[NP];      // last visible position of the lane's row (-1: padding row)
     int lim_min;      // last position visible to every real row (L - T), wave-uniform
+    // one 8-row group: the lane's Q^T operands of the 8 K steps stay in registers for the whole item (32 VGPRs);
+    // more groups read them from LDS per tile
+    half8 qf[NP == 1 ? 8 : 1];
 };
 
 // query rows in LDS: fp16 [RP][256] with 16-byte chunk c of row r stored at chunk c ^ (r % 16)
@@ -396,8 +407,8 @@ struct NoHook {
 // LATE_V: raw.v is unset on entry; load_v(raw, n, q) reads the V operands from the stage after the scores, and after_v()
 // (which refills the stage) runs once they are in registers -- K and V are never live together next to the state
 template <int NP, int KB, int VB, bool LATE_V = false, typename FV = NoHook, typename FA = NoHook>
-__device__ __forceinline__ void compute_tile(WaveState<NP> & st, const half8 * sQ, int p0, RawTile<KB, VB> & raw,
-                                             FV load_v = FV(), FA after_v = FA()) {
+__device__ __forceinline__ void compute_tile(WaveState<NP> & st, const half8 * sQ, int p0, RawTile<KB, VB> & raw, FV load_v = FV(),
+                                             FA after_v = FA()) {
     int lane = lane_id(); // opaque: lane-derived LDS addresses are recomputed per tile, not held across the loop
     asm volatile("" : "+v"(lane));
     const int q = lane >> 4, n = lane & 15;
@@ -411,7 +422,7 @@ __device__ __forceinline__ void compute_tile(WaveState<NP> & st, const half8 * s
         const half8 a1 = kfrag<KB>(raw.k1, ks);
 #pragma unroll
         for (int h = 0; h < NP; h++) {
-            const half8 b = sQ[qchunk(8 * h + (n >> 1), 8 * q + ks)];
+            const half8 b = NP == 1 ? st.qf[ks] : sQ[qchunk(8 * h + (n >> 1), 8 * q + ks)];
             s[h][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, b, s[h][0], 0, 0, 0);
             s[h][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, b, s[h][1], 0, 0, 0);
         }
@@ -421,7 +432,8 @@ __device__ __forceinline__ void compute_tile(WaveState<NP> & st, const half8 * s
     // O, l keep their scale, so most tiles need no rescale of O.  A function of the data order within the fixed
     // partition only: deterministic.
     constexpr float RESCALE_LOG2 = 8.f;
-    const bool full = p0 + ATP - 1 <= st.lim_min; // every position of the tile visible to every row (uniform)
+    // every position of the tile visible to every row (uniform: a scalar branch, no per-value mask on full tiles)
+    const bool full = __builtin_amdgcn_readfirstlane(p0 + ATP - 1 <= st.lim_min);
     // B operands of the two 16-position groups G: (P, 0) in even columns, (0, P) in odd ones; built per row group
     // right after its softmax so that only the packed fp16 P stays live
     const unsigned odd = n & 1;
@@ -433,12 +445,20 @@ __device__ __forceinline__ void compute_tile(WaveState<NP> & st, const half8 * s
     for (int h = 0; h < NP; h++) {
         float t[8];
         float mx = -INFINITY;
+        if (full) {
 #pragma unroll
-        for (int e = 0; e < 8; e++) {
-            const int pos = p0 + (e < 4 ? 4 * q + e : 16 + 4 * q + e - 4);
-            const float sv = (e < 4 ? s[h][0][e] : s[h][1][e - 4]) * LOG2E;
-            t[e] = full || pos <= st.lim[h] ? sv : -INFINITY;
-            mx = fmaxf(mx, t[e]);
+            for (int e = 0; e < 8; e++) {
+                t[e] = (e < 4 ? s[h][0][e] : s[h][1][e - 4]) * LOG2E;
+                mx = fmaxf(mx, t[e]);
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const int pos = p0 + (e < 4 ? 4 * q + e : 16 + 4 * q + e - 4);
+                const float sv = (e < 4 ? s[h][0][e] : s[h][1][e - 4]) * LOG2E;
+                t[e] = pos <= st.lim[h] ? sv : -INFINITY;
+                mx = fmaxf(mx, t[e]);
+            }
         }
         mx = quad_max(mx);
         const float mold = st.m[h];
@@ -577,10 +597,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SMALL ? 3 :
         const SideLayout & SV = S.side[a.layer0 + l][1];
         const size_t ring0 = (size_t) (seq * NKV + g) * S.kvrc;
 
-        auto issue = [&](int i) {
+        // tile i of the wave starts at position c0 + 32 (wv + 4 i); phys: its physical page
+        auto issue = [&](int i, int phys) {
             const int p0 = c0 + ATP * (wv + AWAVES * i), nv = min(ATP, L - p0);
             const bool ring = S.kvrc > 0 && p0 >= ws; // the window: q8 rows (ring, or the main store of q8 sides)
-            const TileSrc t = tile_src<KB, VB>(S, SK, SV, seq, g, p0, ring0, ring);
+            const TileSrc t = tile_src<KB, VB>(S, SK, SV, g, p0, phys, ring0, ring);
             int ln = lane; // opaque: the per-lane chunk addresses are not hoisted out of the tile loop into registers
             asm volatile("" : "+v"(ln));
             if (ring) {
@@ -591,7 +612,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SMALL ? 3 :
             }
         };
 
-        if (my > 0) issue(0);
+        auto tile_page = [&](int i) { return page_of(S, seq, c0 + ATP * (wv + AWAVES * i)); };
+        int phys_cur = my > 0 ? tile_page(0) : 0; // page of the tile in the stage (tile i while step i runs)
+        if (my > 0) issue(0, phys_cur);
         // ---- queries: FWHT when K is stored rotated, * 1/16, fp16 (qwen38_mk.cu:2873-2880), rows r = hh T + t
         for (int r = wv; r < RP; r += AWAVES) {
             half2v o0 = {(_Float16) 0.f, (_Float16) 0.f}, o1 = o0;
@@ -620,11 +643,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SMALL ? 3 :
         }
         st.lim_min = L - T;
         __syncthreads(); // the query rows are complete
+        if constexpr (NP == 1) {
+#pragma unroll
+            for (int ks = 0; ks < 8; ks++) st.qf[ks] = sQ[qchunk(n >> 1, 8 * q + ks)];
+        }
         const uint8_t * const stp = smem + wv * SB; // (derived from smem: LDS reads)
         // one tile: operands into registers, then the stage is free and the next tile streams in during the math
         auto step = [&](auto fmt, int i) {
             constexpr int K2 = decltype(fmt)::kb, V2 = decltype(fmt)::vb;
             set_prio(my - i);
+            const int phys_next = i + 1 < my ? tile_page(i + 1) : 0; // the scalar load overlaps the wait below
             vm_wait<0>(); // tile i has landed (the wave's only copies in flight)
             RawTile<K2, V2> raw;
             const int p0 = c0 + ATP * (wv + AWAVES * i);
@@ -633,7 +661,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SMALL ? 3 :
                 read_k<8, 8>(raw, stp, sc, n, q);
                 lds_drain(); // the K rows are in registers: the V half may overwrite them
                 {
-                    const TileSrc t = tile_src<KB, VB>(S, SK, SV, seq, g, p0, ring0, true);
+                    const TileSrc t = tile_src<KB, VB>(S, SK, SV, g, p0, phys_cur, ring0, true);
                     int ln = lane;
                     asm volatile("" : "+v"(ln));
                     issue_q8_part<1>(t, min(ATP, L - p0), st_lds, ln);
@@ -645,22 +673,23 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SMALL ? 3 :
                         read_v<8, 8>(r, stp, sc + 8 * ATP, tn, tq);
                     },
                     [&]() {
-                        if (i + 1 < my) issue(i + 1);
+                        if (i + 1 < my) issue(i + 1, phys_next);
                     });
             } else if constexpr (LATE_V) {
                 read_k<K2, V2>(raw, stp, n, q);
                 compute_tile<NP, K2, V2, true>(
                     st, sQ, p0, raw, [&](RawTile<K2, V2> & r, int tn, int tq) { read_v<K2, V2>(r, stp, tn, tq); },
                     [&]() {
-                        if (i + 1 < my) issue(i + 1);
+                        if (i + 1 < my) issue(i + 1, phys_next);
                     });
             } else {
                 read_k<K2, V2>(raw, stp, n, q);
                 read_v<K2, V2>(raw, stp, n, q);
                 lds_drain();
-                if (i + 1 < my) issue(i + 1);
+                if (i + 1 < my) issue(i + 1, phys_next);
                 compute_tile<NP, K2, V2>(st, sQ, p0, raw);
             }
+            phys_cur = phys_next;
         };
         // the wave's window (ring) tiles are its last ones: i >= i_ring, p0 >= ws.  Two loops, one tile format each,
         // keep a single tile body live per loop (one body holding both formats costs registers)
@@ -782,21 +811,37 @@ __device__ __forceinline__ void finish_row(float (&v)[4], bool vrot, const float
 }
 
 // ------------------------------------------------------------------------------------------------ combine
-// One workgroup per output row (layer, sequence, kv head, row r): the merge of the head's segment partials
-// (attn_combine, qwen38_mk.cu:4617-4700: y = sum_c e_c O_c / sum_c e_c l_c with e_c = exp(m_c - M)).  Wave w loads the
-// segments c = w, w+4, .. at once, weights them by exp2(m_c - M_w) against its own maximum M_w and sums them in
-// segment order; the four wave sums are rescaled to M = max M_w and added in wave order; y = O / l, then the V
-// un-rotation when V is stored rotated.  The order is fixed by the segment index alone.
-__global__ __launch_bounds__(256) void k_combine(AttnArgs a) {
-    __shared__ float4 s_num[AWAVES][64];
-    __shared__ float2 s_md[AWAVES]; // (max, denominator) of each wave's segments
-    const int R = a.R, T = a.T;
-    int b = blockIdx.x;
-    const int r = b % R;
-    b /= R;
-    const int g = b % NKV;
+// The merge of a head's segment partials (attn_combine, qwen38_mk.cu:4617-4700: y = sum_c e_c O_c / sum_c e_c l_c with
+// e_c = exp(m_c - M)), in two forms with fixed orders (no bit depends on scheduling):
+//   row form   (combine_row)  one workgroup per output row (layer, sequence, kv head, row r).  Wave w loads the
+//              segments c = w, w+4, .. at once, weights them by exp2(m_c - M_w) against its own maximum M_w and sums
+//              them in segment order; the four wave sums are rescaled to M = max M_w and added in wave order; y = O / l,
+//              then the V un-rotation, gate and o_proj units (finish_row).
+//   split form (combine_split) one workgroup per (output row, 64-dim quarter), for launches without rotated V, gate or
+//              units.  Lane group s = 4 w + l / 16 takes the segments c = s, s + 16, .. and sums them the same way;
+//              the 4 groups of a wave are merged by permlane swaps, the 4 waves in wave order.
+// Both run as a kernel of their own after the attention launch (an in-launch merge by extra workgroups that wait for
+// a head's segments measured slower: partials then have to be written through to the coherence point shared by the
+// XCDs before the waiting workgroup may read them).  scratch: LDS of 4 KiB + 32 B.
+// the output row of combine workgroup b of a launch: (layer, sequence, kv head, row r) with r fastest
+struct CombineRow {
+    int l, si, g, r;
+};
+__device__ __forceinline__ CombineRow combine_row_of(const AttnArgs & a, int b) {
+    CombineRow c;
+    c.r = b % a.R;
+    b /= a.R;
+    c.g = b % NKV;
     b /= NKV;
-    const int si = b % a.nseq, l = b / a.nseq;
+    c.si = b % a.nseq;
+    c.l = b / a.nseq;
+    return c;
+}
+
+__device__ __forceinline__ void combine_row(const AttnArgs & a, const CombineRow & cr, uint8_t * scratch) {
+    float4 (*s_num)[64] = reinterpret_cast<float4 (*)[64]>(scratch);         // [AWAVES][64]
+    float2 * s_md = reinterpret_cast<float2 *>(scratch + AWAVES * 64 * 16); // [AWAVES] (max, denominator)
+    const int R = a.R, T = a.T, r = cr.r, g = cr.g, si = cr.si, l = cr.l;
     const SeqDesc & sd = a.sd[si];
     const int nseg = sd.nseg;
     const size_t head0 = (size_t) sd.item0 + (size_t) (l * NKV + g) * nseg;
@@ -834,47 +879,36 @@ __global__ __launch_bounds__(256) void k_combine(AttnArgs a) {
     s_num[wv][lane] = num;
     if (lane == 0) s_md[wv] = make_float2(Mw, den);
     __syncthreads();
-    if (wv != 0) return;
-    // the 4 wave sums in wave order, each rescaled to the overall max
-    float M = s_md[0].x;
+    if (wv == 0) {
+        // the 4 wave sums in wave order, each rescaled to the overall max
+        float M = s_md[0].x;
 #pragma unroll
-    for (int k = 1; k < AWAVES; k++) M = fmaxf(M, s_md[k].x);
-    float4 y = make_float4(0.f, 0.f, 0.f, 0.f);
-    float dd = 0.f;
+        for (int k = 1; k < AWAVES; k++) M = fmaxf(M, s_md[k].x);
+        float4 y = make_float4(0.f, 0.f, 0.f, 0.f);
+        float dd = 0.f;
 #pragma unroll
-    for (int k = 0; k < AWAVES; k++) {
-        const float2 md = s_md[k];
-        const float e = md.x == -INFINITY ? 0.f : exp2f(md.x - M);
-        const float4 z = s_num[k][lane];
-        y.x = __builtin_fmaf(e, z.x, y.x);
-        y.y = __builtin_fmaf(e, z.y, y.y);
-        y.z = __builtin_fmaf(e, z.z, y.z);
-        y.w = __builtin_fmaf(e, z.w, y.w);
-        dd = __builtin_fmaf(e, md.y, dd);
+        for (int k = 0; k < AWAVES; k++) {
+            const float2 md = s_md[k];
+            const float e = md.x == -INFINITY ? 0.f : exp2f(md.x - M);
+            const float4 z = s_num[k][lane];
+            y.x = __builtin_fmaf(e, z.x, y.x);
+            y.y = __builtin_fmaf(e, z.y, y.y);
+            y.z = __builtin_fmaf(e, z.z, y.z);
+            y.w = __builtin_fmaf(e, z.w, y.w);
+            dd = __builtin_fmaf(e, md.y, dd);
+        }
+        float v[4] = {y.x / dd, y.y / dd, y.z / dd, y.w / dd};
+        const int h = GQA * g + r / T, t = r % T;
+        const size_t trow = (size_t) (l * a.nseq + si) * T + t; // the token's row of 24 x 256 outputs
+        finish_row(v, (a.vrot >> (a.layer0 + l)) & 1u, a.gate ? a.gate + (trow * NH + h) * a.gs : nullptr, a.out + (trow * NH + h) * HD,
+                   a.q32a, a.q32b, a.q32m, trow, h);
     }
-    float v[4] = {y.x / dd, y.y / dd, y.z / dd, y.w / dd};
-    const int h = GQA * g + r / T, t = r % T;
-    const size_t trow = (size_t) (l * a.nseq + si) * T + t; // the token's row of 24 x 256 outputs
-    finish_row(v, (a.vrot >> (a.layer0 + l)) & 1u, a.gate ? a.gate + (trow * NH + h) * a.gs : nullptr, a.out + (trow * NH + h) * HD,
-               a.q32a, a.q32b, a.q32m, trow, h);
 }
 
-// The same merge for launches without rotated V, spread wider: one workgroup per (output row, 64-dim quarter).  Lane
-// group s = 4 w + l / 16 (16 per workgroup) takes the segments c = s, s + 16, .. (all loads at once), weights them by
-// exp2(m_c - M_s) against its own maximum and sums them in segment order; the 4 groups of a wave are merged by
-// permlane swaps, the 4 waves in wave order, each sum rescaled to the overall maximum; y = O / l.
-__global__ __launch_bounds__(256) void k_combine_split(AttnArgs a) {
-    __shared__ float4 s_num[AWAVES][16];
-    __shared__ float2 s_md[AWAVES];
-    const int R = a.R, T = a.T;
-    int b = blockIdx.x;
-    const int dq = b & 3;
-    b >>= 2;
-    const int r = b % R;
-    b /= R;
-    const int g = b % NKV;
-    b /= NKV;
-    const int si = b % a.nseq, l = b / a.nseq;
+__device__ __forceinline__ void combine_split(const AttnArgs & a, const CombineRow & cr, int dq, uint8_t * scratch) {
+    float4 (*s_num)[16] = reinterpret_cast<float4 (*)[16]>(scratch);        // [AWAVES][16]
+    float2 * s_md = reinterpret_cast<float2 *>(scratch + AWAVES * 16 * 16); // [AWAVES]
+    const int R = a.R, T = a.T, r = cr.r, g = cr.g, si = cr.si, l = cr.l;
     const SeqDesc & sd = a.sd[si];
     const int nseg = sd.nseg;
     const size_t head0 = (size_t) sd.item0 + (size_t) (l * NKV + g) * nseg;
@@ -919,32 +953,48 @@ __global__ __launch_bounds__(256) void k_combine_split(AttnArgs a) {
     if (sub == 0) s_num[wv][dl] = num;
     if (lane == 0) s_md[wv] = make_float2(Mw, den);
     __syncthreads();
-    if (wv != 0 || sub != 0) return;
-    float M = s_md[0].x;
+    if (wv == 0 && sub == 0) {
+        float M = s_md[0].x;
 #pragma unroll
-    for (int k = 1; k < AWAVES; k++) M = fmaxf(M, s_md[k].x);
-    float4 y = make_float4(0.f, 0.f, 0.f, 0.f);
-    float dd = 0.f;
+        for (int k = 1; k < AWAVES; k++) M = fmaxf(M, s_md[k].x);
+        float4 y = make_float4(0.f, 0.f, 0.f, 0.f);
+        float dd = 0.f;
 #pragma unroll
-    for (int k = 0; k < AWAVES; k++) {
-        const float2 md = s_md[k];
-        const float e = md.x == -INFINITY ? 0.f : exp2f(md.x - M);
-        const float4 z = s_num[k][dl];
-        y.x = __builtin_fmaf(e, z.x, y.x);
-        y.y = __builtin_fmaf(e, z.y, y.y);
-        y.z = __builtin_fmaf(e, z.z, y.z);
-        y.w = __builtin_fmaf(e, z.w, y.w);
-        dd = __builtin_fmaf(e, md.y, dd);
+        for (int k = 0; k < AWAVES; k++) {
+            const float2 md = s_md[k];
+            const float e = md.x == -INFINITY ? 0.f : exp2f(md.x - M);
+            const float4 z = s_num[k][dl];
+            y.x = __builtin_fmaf(e, z.x, y.x);
+            y.y = __builtin_fmaf(e, z.y, y.y);
+            y.z = __builtin_fmaf(e, z.z, y.z);
+            y.w = __builtin_fmaf(e, z.w, y.w);
+            dd = __builtin_fmaf(e, md.y, dd);
+        }
+        const int h = GQA * g + r / T, t = r % T;
+        *reinterpret_cast<float4 *>(a.out + (((size_t) (l * a.nseq + si) * T + t) * NH + h) * HD + dim) =
+            make_float4(y.x / dd, y.y / dd, y.z / dd, y.w / dd);
     }
-    const int h = GQA * g + r / T, t = r % T;
-    *reinterpret_cast<float4 *>(a.out + (((size_t) (l * a.nseq + si) * T + t) * NH + h) * HD + dim) =
-        make_float4(y.x / dd, y.y / dd, y.z / dd, y.w / dd);
+}
+
+__global__ __launch_bounds__(256) void k_combine(AttnArgs a) {
+    __shared__ __attribute__((aligned(16))) uint8_t scratch[AWAVES * 64 * 16 + AWAVES * 8];
+    combine_row(a, combine_row_of(a, blockIdx.x), scratch);
+}
+
+__global__ __launch_bounds__(256) void k_combine_split(AttnArgs a) {
+    __shared__ __attribute__((aligned(16))) uint8_t scratch[AWAVES * 16 * 16 + AWAVES * 8];
+    combine_split(a, combine_row_of(a, blockIdx.x >> 2), blockIdx.x & 3, scratch);
+}
+
+// launches whose rows need the whole row in one workgroup (V stored rotated, gate, o_proj units) use the row form
+static bool host_combine_needs_rows(const AttnArgs & a) {
+    const unsigned vrot = (a.vrot >> a.layer0) & ((a.nl >= 32 ? 0u : 1u << a.nl) - 1u);
+    return vrot || a.gate || a.q32a;
 }
 
 hipError_t launch_combine(const AttnArgs & a, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {
     const unsigned rows = (unsigned) (a.nl * a.nseq * NKV * a.R);
-    const unsigned vrot = (a.vrot >> a.layer0) & ((a.nl >= 32 ? 0u : 1u << a.nl) - 1u);
-    if (vrot || a.gate || a.q32a) hipExtLaunchKernelGGL(k_combine, dim3(rows), dim3(256), 0, st, ev0, ev1, 0, a);
+    if (host_combine_needs_rows(a)) hipExtLaunchKernelGGL(k_combine, dim3(rows), dim3(256), 0, st, ev0, ev1, 0, a);
     else hipExtLaunchKernelGGL(k_combine_split, dim3(4 * rows), dim3(256), 0, st, ev0, ev1, 0, a);
     return hipGetLastError();
 }
@@ -1074,7 +1124,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         const int q0 = min(8 * pw, nv - 1), nq = min(8, nv - q0), p0 = p0t + q0;
         const unsigned lds = (unsigned) __builtin_amdgcn_readfirstlane(lds0 + ((i & 1) * 4 + pw) * PQ_REGION);
         const bool ring = is_ring(i);
-        const TileSrc t = tile_src<KB, VB>(S, SK, SV, a.seq, g, p0, ring0, ring);
+        const TileSrc t = tile_src<KB, VB>(S, SK, SV, g, p0, page_of(S, a.seq, p0), ring0, ring);
         if (ring) pq_issue<8, 8>(t, nq, lds, lane);
         else pq_issue<KB, VB>(t, nq, lds, lane);
     };

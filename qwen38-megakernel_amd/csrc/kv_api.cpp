@@ -521,6 +521,12 @@ static int attend_impl(void * h, int layer0, int n_layers, int n_seq, const int 
             d.cs = seg_len(L);
             d.nseg = (L + d.cs - 1) / d.cs;
             seg_total += d.nseg;
+            // pages pbase, pbase + 1, .. for every logical page the context touches: no table lookups in the kernel
+            const int * pt = s.ptab.data() + (size_t) d.seq * s.pt_stride;
+            const int npg = (L + s.page - 1) / s.page;
+            d.pbase = pt[0];
+            for (int k = 1; k < npg && d.pbase >= 0; k++)
+                if (pt[k] != pt[0] + k) d.pbase = -1;
         }
         if (qnw) {
             if (!s.rope) use_default_rope(s);
@@ -559,6 +565,8 @@ static int attend_impl(void * h, int layer0, int n_layers, int n_seq, const int 
             AttnArgs b = a;
             b.layer0 = layer0 + l;
             b.nl = e - l;
+            b.side0[0] = s.S.side[b.layer0][0];
+            b.side0[1] = s.S.side[b.layer0][1];
             int item = 0;
             for (int i = 0; i < n_seq; i++) {
                 b.sd[i].item0 = item;

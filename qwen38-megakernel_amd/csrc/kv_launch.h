@@ -14,9 +14,12 @@ struct SeqDesc {
     int cs;    // canonical segment length (a function of L's 640-bucket only)
     int nseg;  // segments: ceil(L / cs) <= 128
     int item0; // first work item of this sequence in the launch
+    int pbase; // >= 0: the sequence's pages are pbase, pbase + 1, .. (no table lookup); -1: read the page table
 };
 
 struct AttnArgs {
+    // first: what a workgroup needs before its first tile copy, at fixed offsets (one round of scalar loads)
+    SideLayout side0[2]; // K, V layouts of slot layer0 (S.side[layer0])
     StoreLayout S;
     int layer0;          // first slot of the launch
     int nl;              // layers in the launch (all with the same K/V bits)

@@ -20,8 +20,43 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
 
-__device__ __forceinline__ float shfl_xor(float v, int m) { return __shfl_xor(v, m, 64); }
-__device__ __forceinline__ unsigned shfl_xor_u(unsigned v, int m) { return (unsigned) __shfl_xor((int) v, m, 64); }
+// The value of lane l ^ M, by VALU lane exchanges instead of ds_bpermute (an LDS round trip per exchange): DPP
+// quad_perm for M = 1, 2; quad_perm + row_half_mirror (l ^ 3 ^ 7) for 4; row_mirror + row_half_mirror (l ^ 15 ^ 7)
+// for 8; v_permlane16_swap / v_permlane32_swap for 16 / 32, which leave the partner row's value in one of the two
+// registers depending on the lane's row (inline assembly: the builtin folds the two results when both inputs are the
+// same value; s_nop covers the VALU-write -> permlane-read hazard).
+template <int M>
+__device__ __forceinline__ unsigned xor_lane_u(unsigned v) {
+    if constexpr (M == 1) return __builtin_amdgcn_update_dpp(0u, v, 0xB1, 0xf, 0xf, false); // quad_perm 1,0,3,2
+    else if constexpr (M == 2) return __builtin_amdgcn_update_dpp(0u, v, 0x4E, 0xf, 0xf, false); // quad_perm 2,3,0,1
+    else if constexpr (M == 4) {
+        const unsigned x = __builtin_amdgcn_update_dpp(0u, v, 0x1B, 0xf, 0xf, false); // quad_perm 3,2,1,0
+        return __builtin_amdgcn_update_dpp(0u, x, 0x141, 0xf, 0xf, false);              // row_half_mirror
+    } else if constexpr (M == 8) {
+        const unsigned x = __builtin_amdgcn_update_dpp(0u, v, 0x140, 0xf, 0xf, false); // row_mirror
+        return __builtin_amdgcn_update_dpp(0u, x, 0x141, 0xf, 0xf, false);             // row_half_mirror
+    } else if constexpr (M == 16) {
+        unsigned a = v, b = v;
+        asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+        return (threadIdx.x & 16) ? a : b;
+    } else {
+        static_assert(M == 32, "lane exchange masks 1..32");
+        unsigned a = v, b = v;
+        asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+        return (threadIdx.x & 32) ? a : b;
+    }
+}
+__device__ __forceinline__ unsigned shfl_xor_u(unsigned v, int m) {
+    switch (m) { // m is a constant after unrolling
+    case 1: return xor_lane_u<1>(v);
+    case 2: return xor_lane_u<2>(v);
+    case 4: return xor_lane_u<4>(v);
+    case 8: return xor_lane_u<8>(v);
+    case 16: return xor_lane_u<16>(v);
+    default: return xor_lane_u<32>(v);
+    }
+}
+__device__ __forceinline__ float shfl_xor(float v, int m) { return __builtin_bit_cast(float, shfl_xor_u(__builtin_bit_cast(unsigned, v), m)); }
 
 // max / sum over the four lanes l, l ^ 16, l ^ 32, l ^ 48 with v_permlane16_swap / v_permlane32_swap (VALU exchanges
 // between 16-lane rows, no LDS round trip).  Two copies of the value go in; afterwards one register holds rows

@@ -122,6 +122,23 @@ def bench_cfg3(torch, qkv, steps, warmup):
     t_fused = timed(torch, step_fused, steps, warmup)
     prof_f = profiled(torch, st, step_fused, steps)
     fused_attn_avg = prof_f["attn_ms"] / prof_f["calls"] * 1e-3
+    # a decode slot per layer: store this step's K/V row (position L-1, rewritten every step so L stays fixed) and
+    # attend -- as two calls (append, attend) and as one launch (mk_kv_append_attend)
+    kn = torch.randn(nl, NKV, HD, device="cuda", dtype=torch.float16, generator=g)
+    vn = torch.randn(nl, NKV, HD, device="cuda", dtype=torch.float16, generator=g)
+    kp, vp, rl = kn.data_ptr(), vn.data_ptr(), NKV * HD * 2
+
+    def slot_separate():
+        for l in range(nl):
+            st.append(0, l, 1, L - 1, 1, kp + l * rl, vp + l * rl, 1)
+            st.attend(l, 1, [0], [L], 1, qp + l * lay, op + l * lay)
+
+    def slot_fused():
+        for l in range(nl):
+            st.append_attend(l, 1, [0], [L], 1, kp + l * rl, vp + l * rl, 1, qp + l * lay, op + l * lay)
+
+    t_slot_sep = timed(torch, slot_separate, steps, warmup)
+    t_slot_fused = timed(torch, slot_fused, steps, warmup)
     ok = bool(torch.isfinite(out).all().item())
     return {
         "L": L, "ws": ws, "ring_positions": L - ws, "layers": nl,
@@ -131,7 +148,8 @@ def bench_cfg3(torch, qkv, steps, warmup):
         "combine_avg_s": prof["combine_ms"] / calls * 1e-3, "profiled_step_s": prof["step_s"],
         "fused16_step_s": t_fused, "fused16_positions_per_s": nl * L / t_fused,
         "fused16_gbps": nl * per_layer_bytes / t_fused / 1e9, "fused16_attn_kernel_avg_s": fused_attn_avg,
-        "fused16_attn_kernel_gbps": nl * per_layer_bytes / fused_attn_avg / 1e9, "finite": ok,
+        "fused16_attn_kernel_gbps": nl * per_layer_bytes / fused_attn_avg / 1e9,
+        "slot_append_then_attend_step_s": t_slot_sep, "slot_append_attend_fused_step_s": t_slot_fused, "finite": ok,
     }
 
 

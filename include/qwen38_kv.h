@@ -68,6 +68,17 @@ int mk_kv_attend(void * h, int layer0, int n_layers, int n_seq, const int * seqs
                  void * stream);
 
 /*
+ * mk_kv_append followed by mk_kv_attend in one launch: the T new rows of every sequence (positions lens[i] - T ..
+ * lens[i] - 1; k, v device [n_seq][T][n_layers][4][256] of fp32 (dtype 0) or fp16 (dtype 1), rows after RMSNorm/RoPE)
+ * are stored by the attention kernel itself -- by the wave whose tiles hold them, before those tiles are copied --
+ * and the queries attend over the store including them.  Same stored bytes and outputs as the two calls; one launch
+ * fewer per decode slot (the reference stores the step's K/V inside its attention work items, qwen38_mk.cu:2915-2923,
+ * 3512-3519, 4126-4133).  lens[i] - T must not exceed the stored length (no gap).
+ */
+int mk_kv_append_attend(void * h, int layer0, int n_layers, int n_seq, const int * seqs, const int * lens, int T, const void * k, const void * v,
+                        int dtype, const float * q, float * out, void * stream);
+
+/*
  * mk_kv_attend that allocates nothing: no hipMalloc / hipFree, no host heap.  No counterpart in the reference; for
  * callers that cannot allocate (code under HIP graph capture, tight serving loops).  The segment partials go to a
  * 64 MiB device array the library holds on each GPU it runs on (looked up on the first call on a device, which must be

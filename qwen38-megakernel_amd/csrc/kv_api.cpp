@@ -475,11 +475,15 @@ static int append_impl(void * h, int seq, int layer0, int n_layers, int pos, int
 // qs / gs: row strides (floats) of q and gate; qnw: q-norm weights (the Q prep) or null
 // ws (optional): a caller-provided workspace of ws_bytes for the segment partials, used instead of the store's own
 // (grown on demand) so that the call allocates nothing
+// kin / vin (optional): the fused append of mk_kv_append_attend, [n_seq][T][n_layers][4][256] of dtype kdtype
 static int attend_impl(void * h, int layer0, int n_layers, int n_seq, const int * seqs, const int * lens, int T, const float * q,
                        int qs, const float * qnw, const float * gate, int gs, float * out, int8_t * q32a, int8_t * q32b, uint16_t * q32m,
-                       void * stream, void * ws = nullptr, size_t ws_bytes = 0) {
+                       void * stream, void * ws = nullptr, size_t ws_bytes = 0, const void * kin = nullptr, const void * vin = nullptr,
+                       int kdtype = 0) {
     return guarded([&] {
         Store & s = *as_store(h);
+        if ((kin != nullptr) != (vin != nullptr)) throw std::runtime_error("null K/V pointer");
+        if (kin && kdtype != 0 && kdtype != 1) throw std::runtime_error("dtype: 0 fp32, 1 fp16");
         if ((q32a != nullptr) != (q32b != nullptr) || (q32a != nullptr) != (q32m != nullptr))
             throw std::runtime_error("the q32 outputs come as a set: a, b and meta");
         check_layers(s, layer0, n_layers);
@@ -506,14 +510,19 @@ static int attend_impl(void * h, int layer0, int n_layers, int n_seq, const int 
             if (L < T || L > s.ctx) throw std::runtime_error("context length " + std::to_string(L) + " outside T .. ctx");
             if ((L - T + ATT_BUCKET_) / ATT_BUCKET_ != (L - 1 + ATT_BUCKET_) / ATT_BUCKET_)
                 throw std::runtime_error("the T rows straddle a 640-position bucket (cap T with mk_kv_cap_T)");
-            if (L > s.n[seqs[i]])
+            // with the fused append the call stores positions L - T .. L - 1 first: no gap after the stored rows
+            const int n_after = kin ? std::max(s.n[seqs[i]], L) : s.n[seqs[i]], top_after = kin ? std::max(s.top[seqs[i]], L) : s.top[seqs[i]];
+            if (kin && L - T > s.n[seqs[i]])
+                throw std::runtime_error("appending from position " + std::to_string(L - T) + " leaves a gap after the " +
+                                         std::to_string(s.n[seqs[i]]) + " stored positions of sequence " + std::to_string(seqs[i]));
+            if (L > n_after)
                 throw std::runtime_error("context length " + std::to_string(L) + " beyond the " + std::to_string(s.n[seqs[i]]) +
                                          " positions stored for sequence " + std::to_string(seqs[i]));
             // the window rows ws .. L-1 are read from the ring, which holds the newest kvrc rows written: rows older
             // than top - kvrc have been overwritten by later appends (rewind first to attend there)
-            if (s.ring_bytes && s.top[seqs[i]] - s.kvrc > window_start(L, s.win))
+            if (s.ring_bytes && top_after - s.kvrc > window_start(L, s.win))
                 throw std::runtime_error("context length " + std::to_string(L) + ": its window rows were overwritten in the ring by " +
-                                         "positions up to " + std::to_string(s.top[seqs[i]] - 1) + " (rewind first)");
+                                         "positions up to " + std::to_string(top_after - 1) + " (rewind first)");
             SeqDesc & d = a.sd[i];
             d.seq = seqs[i];
             d.L = L;
@@ -578,6 +587,13 @@ static int attend_impl(void * h, int layer0, int n_layers, int n_seq, const int 
             b.out = out + (size_t) l * n_seq * T * NH * HD;
             if (gate) b.gate = gate + (size_t) l * n_seq * T * NH * gs;
             if (qnw) b.qnw = qnw + (size_t) l * HD;
+            if (kin) {
+                const size_t esz = kdtype ? 2 : 4;
+                b.kin = static_cast<const char *>(kin) + (size_t) l * NKV * HD * esz;
+                b.vin = static_cast<const char *>(vin) + (size_t) l * NKV * HD * esz;
+                b.kin_nl = n_layers;
+                b.kin_f16 = kdtype;
+            }
             if (q32a) {
                 b.q32a = q32a + (size_t) l * n_seq * T * 192 * 16;
                 b.q32b = q32b + (size_t) l * n_seq * T * 192 * 16;
@@ -596,6 +612,11 @@ static int attend_impl(void * h, int layer0, int n_layers, int n_seq, const int 
             HCK(launch_attn(b, s.S.side[b.layer0][0].bits, s.S.side[b.layer0][1].bits, s.max_blocks, s.occupancy, st, ev(0, g), ev(1, g)));
         }
         for (size_t g = 0; g < ng; g++) HCK(launch_combine(groups[g], st, ev(2, g), ev(3, g)));
+        if (kin)
+            for (int i = 0; i < n_seq; i++) {
+                s.n[seqs[i]] = std::max(s.n[seqs[i]], lens[i]);
+                s.top[seqs[i]] = std::max(s.top[seqs[i]], lens[i]);
+            }
         return 0;
     });
 }
@@ -616,6 +637,16 @@ int mk_kv_append_prep(void * h, int seq, int layer0, int n_layers, int pos, int 
 int mk_kv_attend(void * h, int layer0, int n_layers, int n_seq, const int * seqs, const int * lens, int T, const float * q, float * out,
                  void * stream) {
     return attend_impl(h, layer0, n_layers, n_seq, seqs, lens, T, q, HD, nullptr, nullptr, HD, out, nullptr, nullptr, nullptr, stream);
+}
+
+int mk_kv_append_attend(void * h, int layer0, int n_layers, int n_seq, const int * seqs, const int * lens, int T, const void * k, const void * v,
+                        int dtype, const float * q, float * out, void * stream) {
+    if (!k || !v) {
+        g_err = "null K/V pointer";
+        return -1;
+    }
+    return attend_impl(h, layer0, n_layers, n_seq, seqs, lens, T, q, HD, nullptr, nullptr, HD, out, nullptr, nullptr, nullptr, stream, nullptr, 0,
+                       k, v, dtype);
 }
 
 int mk_kv_attend_noalloc(void * h, int layer0, int n_layers, int n_seq, const int * seqs, const int * lens, int T, const float * q,

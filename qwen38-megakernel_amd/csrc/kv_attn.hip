@@ -638,7 +638,33 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SMALL ? 3 :
             return sd.pbase >= 0 ? sd.pbase + __builtin_amdgcn_readfirstlane(p / spage) : page_of(S, seq, p);
         };
         int phys_cur = my > 0 ? tile_page(0) : 0; // page of the tile in the stage (tile i while step i runs)
+        // fused append: this wave's tiles that hold new positions (L - T .. L - 1) are copied only after the wave has
+        // stored those rows (the vmcnt wait before the copy covers the stores); a new row in tile 0 is stored first
+        int new_tile0 = my; // the wave's first tile holding a new position
+        if (a.kin) {
+            const int pa = max(L - T, c0), pb = min(L, c1);
+            for (int p = pa; p < pb; p++)
+                if (((p - c0) >> 5) % AWAVES == wv) new_tile0 = min(new_tile0, ((p - c0) >> 5) / AWAVES);
+        }
+        auto append_rows = [&]() {
+            const int pa = max(L - T, c0), pb = min(L, c1);
+            for (int p = pa; p < pb; p++) {
+                if (((p - c0) >> 5) % AWAVES != wv) continue;
+                const size_t row = ((((size_t) si * T + (p - (L - T))) * a.kin_nl + l) * NKV + g) * HD;
+#pragma unroll
+                for (int w = 0; w < 2; w++) {
+                    float v[4];
+                    load_row4(w ? a.vin : a.kin, row, a.kin_f16, v);
+                    store_row(S, w ? SV : SK, seq, g, p, true, v);
+                }
+            }
+        };
+        if (new_tile0 == 0) {
+            append_rows();
+            vm_wait<0>(); // the stored rows are in L2 before this wave's copies read them
+        }
         if (my > 0) issue(0, phys_cur);
+        if (new_tile0 > 0 && new_tile0 < my) append_rows(); // stored while the first tiles stream
         // ---- queries: FWHT when K is stored rotated, * 1/16, fp16 (qwen38_mk.cu:2873-2880), rows r = hh T + t
         for (int r = wv; r < RP; r += AWAVES) {
             half2v o0 = {(_Float16) 0.f, (_Float16) 0.f}, o1 = o0;

@@ -191,6 +191,76 @@ __device__ __forceinline__ unsigned quant_qn(const float (&v)[4], int bits, uint
     return codes;
 }
 
+// ------------------------------------------------------------------------------------------------ kv_store of one row
+// One row per wave: lane l holds values 4l .. 4l+3 (kv_store, qwen38_mk.cu:2099-2116).  Used by the append kernel and
+// by the attention kernel's fused append (mk_kv_append_attend), so both store the same bytes.
+
+__device__ __forceinline__ size_t main_row(const StoreLayout & S, int seq, int g, int p) {
+    const int lp = p / S.page;
+    const int phys = S.ptab[seq * S.pt_stride + lp];
+    return (size_t) (g * S.n_pages + phys) * S.page + (p - lp * S.page);
+}
+__device__ __forceinline__ size_t ring_row(const StoreLayout & S, int seq, int g, int p) {
+    return (size_t) (seq * NKV + g) * S.kvrc + p % S.kvrc;
+}
+
+// the lane's 4 values of input row `row` (elements row .. row + 255) of fp16 (f16) or fp32 data
+__device__ __forceinline__ void load_row4(const void * in, size_t row, int f16, float (&v)[4]) {
+    const size_t src = row + 4 * lane_id();
+    if (f16) {
+        const uint2 raw = *reinterpret_cast<const uint2 *>(static_cast<const _Float16 *>(in) + src);
+        const half2v a = __builtin_bit_cast(half2v, raw.x), b = __builtin_bit_cast(half2v, raw.y);
+        v[0] = (float) a[0];
+        v[1] = (float) a[1];
+        v[2] = (float) b[0];
+        v[3] = (float) b[1];
+    } else {
+        const float4 raw = *reinterpret_cast<const float4 *>(static_cast<const float *>(in) + src);
+        v[0] = raw.x;
+        v[1] = raw.y;
+        v[2] = raw.z;
+        v[3] = raw.w;
+    }
+}
+
+// the row of position p (kv head g of sequence seq) on side sd: optional FWHT, the main row in the side's format and,
+// when ring and the side has a window, the q8 ring copy of the same rotated values.  All 64 lanes call it.
+__device__ __forceinline__ void store_row(const StoreLayout & S, const SideLayout & sd, int seq, int g, int p, bool ring, float (&v)[4]) {
+    const int lane = lane_id();
+    if (sd.rot) fwht256_w64(v);
+    const size_t row = main_row(S, seq, g, p);
+    uint16_t sc;
+    if (sd.bits == 8) {
+        const unsigned word = quant_q8(v, sc);
+        *reinterpret_cast<unsigned *>(sd.vals + row * HD + 4 * lane) = word;
+    } else {
+        const int bits = sd.bits, hb = bits - 4, odd = lane & 1;
+        const unsigned codes = quant_qn(v, bits, sc);
+        // word lane/2 of the row: the even lane's values are its low nibbles, the odd lane's the high nibbles
+        unsigned nib = codes & 0x0f0f0f0fu;
+        if (odd) nib <<= 4;
+        unsigned hi = 0;
+#pragma unroll
+        for (int k = 0; k < 4; k++) hi |= ((codes >> (8 * k + 4)) & 0xfu) << (hb * (k + 4 * odd));
+        nib |= shfl_xor_u(nib, 1);
+        hi |= shfl_xor_u(hi, 1);
+        uint8_t * rp = sd.vals + row * row_bytes(bits);
+        if (!odd) {
+            *reinterpret_cast<unsigned *>(rp + 4 * (lane >> 1)) = nib;
+            uint8_t * hp = rp + 128 + (lane >> 1) * hb;
+            for (int k = 0; k < hb; k++) hp[k] = (uint8_t) (hi >> (8 * k));
+        }
+    }
+    if ((lane & 7) == 0) sd.scs[row * 8 + (lane >> 3)] = sc;
+    if (ring && sd.ring) {
+        uint16_t rs;
+        const unsigned word = quant_q8(v, rs);
+        const size_t rr = ring_row(S, seq, g, p);
+        *reinterpret_cast<unsigned *>(sd.ring + rr * HD + 4 * lane) = word;
+        if ((lane & 7) == 0) sd.rsc[rr * 8 + (lane >> 3)] = rs;
+    }
+}
+
 // ------------------------------------------------------------------------------------------------ dequantization
 // fp16 operands are built with the 0x6400 magic: the half with bits 0x6400 | n is 1024 + n exactly (n < 1024), so
 // (0x6400 | n) - (1024 + bias) is the integer code exactly and one fp16 multiply by the scale rounds d * q once,

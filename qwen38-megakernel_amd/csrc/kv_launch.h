@@ -40,6 +40,12 @@ struct AttnArgs {
     uint16_t * q32m;     // ... [nl][nseq][T][192][4]: half scales of the a / b blocks, int sums of the a / b halves
     float * part;        // [item][R][HD] per-segment partial outputs (unnormalised)
     float2 * ml;         // [item][R] per-segment (max in log2 units, sum)
+    // fused append (mk_kv_append_attend): the rows of positions L - T .. L - 1 of every sequence, stored inside this
+    // launch by the wave whose tiles hold them, before those tiles are copied.  kin / vin [nseq][T][kin_nl][NKV][HD]
+    // (fp16 when kin_f16), layer l of the launch at kin_nl index l; nullptr: no append
+    const void * kin;
+    const void * vin;
+    int kin_nl, kin_f16;
 };
 
 // one prefill piece of one layer: query rows r = 6 t + hh (token t = 0 .. Tp-1 at position n0 + t, query head

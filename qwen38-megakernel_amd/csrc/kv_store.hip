@@ -11,80 +11,24 @@
 
 namespace qkv {
 
-__device__ __forceinline__ size_t main_row(const StoreLayout & S, int seq, int g, int p) {
-    const int lp = p / S.page;
-    const int phys = S.ptab[seq * S.pt_stride + lp];
-    return (size_t) (g * S.n_pages + phys) * S.page + (p - lp * S.page);
-}
-__device__ __forceinline__ size_t ring_row(const StoreLayout & S, int seq, int g, int p) {
-    return (size_t) (seq * NKV + g) * S.kvrc + p % S.kvrc;
-}
-
 // One wave per row; lane l holds values 4l .. 4l+3.  Rows of the input: [T][nl][NKV][256] (fp16 or fp32).
 __global__ __launch_bounds__(256) void k_append(StoreLayout S, int seq, int layer0, int nl, int pos, int T, const void * kin,
                                                 const void * vin, int f16, const float * knw, const float2 * rope) {
     const int wave = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (wave >= T * nl * NKV * 2) return;
-    const int lane = threadIdx.x & 63;
     const int w = wave & 1;
     int r = wave >> 1;
     const int g = r % NKV;
     r /= NKV;
     const int l = r % nl, t = r / nl;
-    const size_t src = ((size_t) (t * nl + l) * NKV + g) * HD + 4 * lane;
-    const void * in = w ? vin : kin;
+    const size_t src = ((size_t) (t * nl + l) * NKV + g) * HD;
     float v[4];
-    if (f16) {
-        const uint2 raw = *reinterpret_cast<const uint2 *>(static_cast<const _Float16 *>(in) + src);
-        const half2v a = as_h2(raw.x), b = as_h2(raw.y);
-        v[0] = (float) a[0];
-        v[1] = (float) a[1];
-        v[2] = (float) b[0];
-        v[3] = (float) b[1];
-    } else {
-        const float4 raw = *reinterpret_cast<const float4 *>(static_cast<const float *>(in) + src);
-        v[0] = raw.x;
-        v[1] = raw.y;
-        v[2] = raw.z;
-        v[3] = raw.w;
-    }
-    const SideLayout & sd = S.side[layer0 + l][w];
+    load_row4(w ? vin : kin, src, f16, v);
     const int p = pos + t;
     if (knw && !w) qk_prep(v, knw + (size_t) l * HD, rope + (size_t) p * 32);
-    if (sd.rot) fwht256_w64(v);
-    const size_t row = main_row(S, seq, g, p);
-    uint16_t sc;
-    if (sd.bits == 8) {
-        const unsigned word = quant_q8(v, sc);
-        *reinterpret_cast<unsigned *>(sd.vals + row * HD + 4 * lane) = word;
-    } else {
-        const int bits = sd.bits, hb = bits - 4, odd = lane & 1;
-        const unsigned codes = quant_qn(v, bits, sc);
-        // word lane/2 of the row: the even lane's values are its low nibbles, the odd lane's the high nibbles
-        unsigned nib = codes & 0x0f0f0f0fu;
-        if (odd) nib <<= 4;
-        unsigned hi = 0;
-#pragma unroll
-        for (int k = 0; k < 4; k++) hi |= ((codes >> (8 * k + 4)) & 0xfu) << (hb * (k + 4 * odd));
-        nib |= shfl_xor_u(nib, 1);
-        hi |= shfl_xor_u(hi, 1);
-        uint8_t * rp = sd.vals + row * row_bytes(bits);
-        if (!odd) {
-            *reinterpret_cast<unsigned *>(rp + 4 * (lane >> 1)) = nib;
-            uint8_t * hp = rp + 128 + (lane >> 1) * hb;
-            for (int k = 0; k < hb; k++) hp[k] = (uint8_t) (hi >> (8 * k));
-        }
-    }
-    if ((lane & 7) == 0) sd.scs[row * 8 + (lane >> 3)] = sc;
     // ring copy: only for the newest kvrc positions of the call (p >= pos + T - kvrc); an older one shares its ring
     // row with a newer position of the same launch and is evicted by it anyway, and writing both would race
-    if (sd.ring && p >= pos + T - S.kvrc) {
-        uint16_t rs;
-        const unsigned word = quant_q8(v, rs);
-        const size_t rr = ring_row(S, seq, g, p);
-        *reinterpret_cast<unsigned *>(sd.ring + rr * HD + 4 * lane) = word;
-        if ((lane & 7) == 0) sd.rsc[rr * 8 + (lane >> 3)] = rs;
-    }
+    store_row(S, S.side[layer0 + l][w], seq, g, p, p >= pos + T - S.kvrc, v);
 }
 
 // One wave per (position, layer, side, kv head) of positions p0 .. p1-1.

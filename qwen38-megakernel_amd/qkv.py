@@ -27,6 +27,7 @@ SIGNATURES = {
     "mk_kv_set_pages": (_c_int, [_c_vp, _c_int, _P_int, _c_int]),
     "mk_kv_append": (_c_int, [_c_vp, _c_int, _c_int, _c_int, _c_int, _c_int, _c_vp, _c_vp, _c_int, _c_vp]),
     "mk_kv_attend": (_c_int, [_c_vp, _c_int, _c_int, _c_int, _P_int, _P_int, _c_int, _c_vp, _c_vp, _c_vp]),
+    "mk_kv_append_attend": (_c_int, [_c_vp, _c_int, _c_int, _c_int, _P_int, _P_int, _c_int, _c_vp, _c_vp, _c_int, _c_vp, _c_vp, _c_vp]),
     "mk_kv_attend_noalloc": (_c_int, [_c_vp, _c_int, _c_int, _c_int, _P_int, _P_int, _c_int, _c_vp, _c_vp, _c_vp]),
     "mk_kv_attend_gated": (_c_int, [_c_vp, _c_int, _c_int, _c_int, _P_int, _P_int, _c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _P_u16,
                                     _c_vp]),
@@ -149,6 +150,13 @@ class KVStore:
         s = (ctypes.c_int * n)(*seqs)
         l = (ctypes.c_int * n)(*lens)
         _check(lib().mk_kv_attend(self.h, layer0, n_layers, n, s, l, T, q_ptr, out_ptr, stream))
+
+    def append_attend(self, layer0, n_layers, seqs, lens, T, k_ptr, v_ptr, dtype, q_ptr, out_ptr, stream=0):
+        """append of positions lens[i] - T .. lens[i] - 1 ([n_seq][T][n_layers][4][256]) and attend, in one launch."""
+        n = len(seqs)
+        s = (ctypes.c_int * n)(*seqs)
+        l = (ctypes.c_int * n)(*lens)
+        _check(lib().mk_kv_append_attend(self.h, layer0, n_layers, n, s, l, T, k_ptr, v_ptr, dtype, q_ptr, out_ptr, stream))
 
     def attend_noalloc(self, layer0, n_layers, seqs, lens, T, q_ptr, out_ptr, stream=0):
         """attend with the partials in the library's per-device array (mk_kv_attend_noalloc): allocates nothing."""

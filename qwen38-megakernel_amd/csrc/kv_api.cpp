@@ -140,6 +140,7 @@ struct Store {
     size_t ml_bytes = 0;
     int max_blocks = 0;
     int occupancy = 0; // decode workgroups per CU: 0 = by launch size, 2 or 3 (launch_attn)
+    int wide = 1;      // 25..48 query rows per kv head: one pass of 8-wave workgroups (1) or two batches of 24 rows (0)
     // RoPE table of the Q/K prep calls: [rope_rows][32] (cos, sin), the caller's or the store's own text table
     const float2 * rope = nullptr;
     int rope_rows = 0;
@@ -499,7 +500,8 @@ static int attend_impl(void * h, int layer0, int n_layers, int n_seq, const int 
         a.gs = gs;
         a.qnw = qnw;
         a.R = GQA * T;
-        a.RP = a.R <= 8 ? 8 : a.R <= 16 ? 16 : 24; // T = 1: one 8-row group; T = 2: 16 rows; T >= 3: batches of 24 rows
+        a.RP = a.R <= 8 ? 8 : a.R <= 16 ? 16 : 24; // T = 1: one 8-row group; T = 2: 16 rows; T >= 3: 24 rows per wave
+        a.wide = a.R > 24 && s.wide;               // T >= 5: both halves of 24 rows in one workgroup
         a.nseq = n_seq;
         int seg_total = 0;
         for (int i = 0; i < n_seq; i++) {
@@ -582,7 +584,7 @@ static int attend_impl(void * h, int layer0, int n_layers, int n_seq, const int 
                 item += b.nl * NKV * b.sd[i].nseg;
             }
             b.n_base = item;
-            b.n_items = item * ((a.R + a.RP - 1) / a.RP);
+            b.n_items = item * (a.wide ? 1 : (a.R + a.RP - 1) / a.RP);
             b.q = q + (size_t) l * n_seq * T * NH * qs;
             b.out = out + (size_t) l * n_seq * T * NH * HD;
             if (gate) b.gate = gate + (size_t) l * n_seq * T * NH * gs;
@@ -972,6 +974,11 @@ int mk_kv_config(void * h, const char * key, long long value) {
         if (!strcmp(key, "max_blocks")) {
             if (value < 0) throw std::runtime_error("max_blocks must be >= 0");
             s.max_blocks = (int) value;
+            return 0;
+        }
+        if (!strcmp(key, "wide")) {
+            if (value != 0 && value != 1) throw std::runtime_error("wide must be 0 or 1");
+            s.wide = (int) value;
             return 0;
         }
         if (!strcmp(key, "occupancy")) {

@@ -247,6 +247,14 @@ template <int N>
 __device__ __forceinline__ void vm_wait() {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
+// a 16-byte load the compiler does not track: the caller waits for it with vm_wait and then pins the value (pin_after)
+// -- a tracked load would make the compiler's own wait before the first use also drain the tile copies issued after it
+__device__ __forceinline__ f32x4 gload16(const void * g) {
+    f32x4 r;
+    asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(r) : "v"(g) : "memory");
+    return r;
+}
+__device__ __forceinline__ void pin_after(f32x4 & x) { asm volatile("" : "+v"(x)); }
 struct TileSrc {
     const uint8_t * k;
     const uint16_t * ks;
@@ -282,37 +290,47 @@ __device__ __forceinline__ TileSrc tile_src(const StoreLayout & S, const SideLay
     return t;
 }
 
-// copies of one tile into the stage at LDS address `lds`; returns the number of copy instructions (KB + VB + 1).
+// copies of one tile into the stage at LDS address `lds` (KB + VB + 1 copy instructions per lane).
 // Full tiles copy contiguous bytes (one address add per instruction); the last, partial tile of a context clamps each
 // 16-byte chunk to the last valid row.
-template <int KB, int VB>
-__device__ __forceinline__ int issue_tile(const TileSrc & t, int nv, unsigned lds, int lane) {
+// PART: 0 = the whole tile, 1 = the K rows and scales, 2 = the V rows and scales (two waves sharing one stage, each
+// copying what it stores in a fused append)
+template <int KB, int VB, int PART = 0>
+__device__ __forceinline__ void issue_tile(const TileSrc & t, int nv, unsigned lds, int lane) {
     constexpr int KR = 2 * KB, VR = 2 * VB; // 16-byte chunks per row
+    constexpr bool DK = PART != 2, DV = PART != 1;
     if (nv == ATP) {
         const unsigned off = 16 * lane;
+        if constexpr (DK)
 #pragma unroll
-        for (int j = 0; j < KB; j++) dma16s(t.k + 1024 * j, off, lds + 1024 * j);
+            for (int j = 0; j < KB; j++) dma16s(t.k + 1024 * j, off, lds + 1024 * j);
+        if constexpr (DV)
 #pragma unroll
-        for (int j = 0; j < VB; j++) dma16s(t.v + 1024 * j, off, lds + 1024 * (KB + j));
+            for (int j = 0; j < VB; j++) dma16s(t.v + 1024 * j, off, lds + 1024 * (KB + j));
     } else {
+        if constexpr (DK)
 #pragma unroll
-        for (int j = 0; j < KB; j++) {
-            int c = j * 64 + lane;
-            const int r = c / KR;
-            if (r >= nv) c = (nv - 1) * KR + (c - r * KR);
-            dma16(t.k + 16 * c, lds + 1024 * j);
-        }
+            for (int j = 0; j < KB; j++) {
+                int c = j * 64 + lane;
+                const int r = c / KR;
+                if (r >= nv) c = (nv - 1) * KR + (c - r * KR);
+                dma16(t.k + 16 * c, lds + 1024 * j);
+            }
+        if constexpr (DV)
 #pragma unroll
-        for (int j = 0; j < VB; j++) {
-            int c = j * 64 + lane;
-            const int r = c / VR;
-            if (r >= nv) c = (nv - 1) * VR + (c - r * VR);
-            dma16(t.v + 16 * c, lds + 1024 * (KB + j));
-        }
+            for (int j = 0; j < VB; j++) {
+                int c = j * 64 + lane;
+                const int r = c / VR;
+                if (r >= nv) c = (nv - 1) * VR + (c - r * VR);
+                dma16(t.v + 16 * c, lds + 1024 * (KB + j));
+            }
     }
     const int r = min(lane & 31, nv - 1);
-    dma16(lane < 32 ? static_cast<const void *>(t.ks + 8 * r) : static_cast<const void *>(t.vs + 8 * r), lds + 1024 * (KB + VB));
-    return KB + VB + 1;
+    if constexpr (PART == 0) {
+        dma16(lane < 32 ? static_cast<const void *>(t.ks + 8 * r) : static_cast<const void *>(t.vs + 8 * r), lds + 1024 * (KB + VB));
+    } else if ((lane < 32) == (PART == 1)) { // half the lanes: the same LDS slots (lane-indexed) as the whole copy
+        dma16(PART == 1 ? static_cast<const void *>(t.ks + 8 * r) : static_cast<const void *>(t.vs + 8 * r), lds + 1024 * (KB + VB));
+    }
 }
 
 // a q8 tile through a stage smaller than one (three workgroups per CU): part 0 = the K rows at 0 and every scale at
@@ -555,19 +573,24 @@ __device__ __forceinline__ void set_prio(int left) {
 }
 
 // ------------------------------------------------------------------------------------------------ the kernel
-// More than 16 query rows (T >= 3) run as batches of 24 rows (one pass for T <= 4, two for T = 5..8): work item =
-// (sequence, layer, kv head, segment, row batch), batch-minor; each batch streams the segment's tiles again with the
-// three-group kernel (48 rows of accumulators in one wave spill), and every row sees the same slices, tile arithmetic
-// and merge whatever T.  The batches of a segment run side by side, so the second read mostly hits the last-level
-// cache.
+// More than 16 query rows (T >= 3) are held as 24 rows per wave (three groups; 48 rows of accumulators in one wave
+// spill).  T = 3, 4: one 24-row pass.  T = 5..8: the WIDE kernel below, or (knob) batches of 24 rows: work item =
+// (sequence, layer, kv head, segment, row batch), batch-minor, each batch streaming the segment's tiles again.  Every
+// row sees the same slices, tile arithmetic and merge whatever T and whichever kernel.
+// WIDE (25..48 rows, T = 5..8): one pass instead of two batches.  8 waves: waves w and w + 4 take the same slice of
+// tiles (w, w + 4, ..) for rows 0..23 and 24..47, and share two stages per slice: at step i (after a workgroup barrier)
+// tile i + 1 is copied into the other stage -- the K rows by the first wave of the pair, the V rows by the second --
+// while both compute tile i.  A row's slices, tile arithmetic and merge order are those of the batched kernel.
 // SMALL (one 8-row group, KB + VB <= 11): three workgroups per CU for launches with many work items.  The stages hold
 // one packed tile (32 (KB + VB) + 1 KiB); a q8 window tile goes through in two halves (issue_q8_part); the V operands
 // are read after the scores (168 registers).  Same slices and arithmetic: bitwise the same partials.
-template <int NP, int KB, int VB, bool SMALL = false>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SMALL ? 3 : 2, SMALL ? 3 : 2))) void k_attn(AttnArgs a) {
+template <int NP, int KB, int VB, bool SMALL = false, bool WIDE = false>
+__global__ __launch_bounds__(WIDE ? 512 : 256) __attribute__((amdgpu_waves_per_eu(SMALL ? 3 : 2, SMALL ? 3 : 2))) void k_attn(AttnArgs a) {
     static_assert(!SMALL || (NP == 1 && KB + VB <= 11), "small stages: one row group, packed tiles of at most 11 KiB");
-    constexpr int RP = 8 * NP; // query rows held (the padding rows are zero)
-    constexpr int SB = SMALL ? 1024 * (KB + VB) + 1024 : STAGE_BYTES, SLDS = AWAVES * SB; // stage bytes, all stages
+    static_assert(!WIDE || NP == 3, "wide: two halves of 24 rows");
+    constexpr int RP = 8 * NP;                // query rows held by a wave (the padding rows are zero)
+    constexpr int NW = WIDE ? 2 * AWAVES : AWAVES, NQ = WIDE ? 2 * RP : RP; // waves, query rows of the workgroup
+    constexpr int SB = SMALL ? 1024 * (KB + VB) + 1024 : STAGE_BYTES, SLDS = NW * SB; // stage bytes, all stages
     // NP = 3: the V operands are read from the stage after the scores (the stage is refilled only then), so a wave
     // never holds a whole raw tile in registers next to 24 rows of accumulators, and two workgroups fit a CU
     constexpr bool LATE_V = NP >= 3 || SMALL;
@@ -575,10 +598,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SMALL ? 3 :
     // the wave index as a scalar: tile positions, page lookups and source selection stay scalar (SMEM loads, uniform
     // branches); vector loads there would need vmcnt waits that also drain the tile copies in flight
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63, n = lane & 15, q = lane >> 4;
+    const int sl = WIDE ? wv & (AWAVES - 1) : wv, hf = WIDE ? wv / AWAVES : 0; // the wave's slice of tiles, row half
     const StoreLayout & S = a.S;
     const unsigned lds0 = (unsigned) (size_t) (__attribute__((address_space(3))) uint8_t *) smem;
+    // stage b (0, 1) of the wave's slice: one per wave, or two per slice (WIDE)
+    auto stage_of = [&](int b) { return WIDE ? 2 * sl + b : wv; };
     const unsigned st_lds = (unsigned) __builtin_amdgcn_readfirstlane(lds0 + wv * SB);
-    half8 * const sQ = reinterpret_cast<half8 *>(smem + SLDS); // [RP][256] fp16, chunk-swizzled (qchunk)
+    half8 * const sQ = reinterpret_cast<half8 *>(smem + SLDS); // [NQ][256] fp16, chunk-swizzled (qchunk) per half
+    const half8 * const sQh = sQ + hf * RP * (HD / 8);          // the wave's rows
     // The first tile copy of an item waits on every scalar load before it, and each round trip to the kernel arguments
     // costs a few hundred ns at launch: the common case (one sequence, one layer) needs one round -- the header, sd[0]
     // and side0 at fixed offsets, made live together by the empty asm so that the loads issue back to back and are
@@ -591,7 +618,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SMALL ? 3 :
                  "s"(V0.scs), "s"(V0.ring), "s"(V0.rsc), "s"(a.T), "s"(a.R), "s"(a.layer0), "s"(a.krot), "s"(a.qs), "s"(a.q),
                  "s"(a.qnw), "s"(a.rope), "s"(S.ptab), "s"(S.pt_stride));
     for (int bitem = blockIdx.x; bitem < n_items; bitem += gridDim.x) {
-        const int nb = n_items / n_base, item = bitem / nb, batch = bitem - item * nb, row0 = RP * batch;
+        const int nb = n_items / n_base, item = bitem / nb, batch = bitem - item * nb, row0 = RP * (WIDE ? hf : batch);
         int si = 0;
         SeqDesc sd = sd0;
         if (nseq > 1) {
@@ -609,7 +636,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SMALL ? 3 :
         const int L = sd.L, ws = sd.ws, seq = sd.seq, T = a.T;
         const int c0 = seg * sd.cs, c1 = min(L, c0 + sd.cs);
         const int ntiles = (c1 - c0 + ATP - 1) / ATP;
-        const int my = ntiles > wv ? (ntiles - wv + AWAVES - 1) / AWAVES : 0; // tiles wv, wv+4, ..
+        const int my = ntiles > sl ? (ntiles - sl + AWAVES - 1) / AWAVES : 0; // tiles sl, sl+4, ..
+        const int my0 = (ntiles + AWAVES - 1) / AWAVES;                       // steps of the workgroup (slice 0)
         SideLayout SK = K0, SV = V0;
         if (l > 0) {
             SK = S.side[a.layer0 + l][0];
@@ -617,24 +645,32 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SMALL ? 3 :
         }
         const size_t ring0 = (size_t) (seq * NKV + g) * kvrc;
 
-        // tile i of the wave starts at position c0 + 32 (wv + 4 i); phys: its physical page
-        auto issue = [&](int i, int phys) {
-            const int p0 = c0 + ATP * (wv + AWAVES * i), nv = min(ATP, L - p0);
+        // tile i of the wave starts at position c0 + 32 (sl + 4 i); phys: its physical page; into the stage at lds_to
+        auto issue = [&](int i, int phys, unsigned lds_to) {
+            const int p0 = c0 + ATP * (sl + AWAVES * i), nv = min(ATP, L - p0);
             const bool ring = S.kvrc > 0 && p0 >= ws; // the window: q8 rows (ring, or the main store of q8 sides)
             const TileSrc t = tile_src<KB, VB>(S, SK, SV, g, p0, phys, ring0, ring);
             int ln = lane; // opaque: the per-lane chunk addresses are not hoisted out of the tile loop into registers
             asm volatile("" : "+v"(ln));
-            if (ring) {
-                if constexpr (SMALL) issue_q8_part<0>(t, nv, st_lds, ln);
-                else issue_tile<8, 8>(t, nv, st_lds, ln);
+            if constexpr (WIDE) {
+                if (ring) {
+                    if (hf == 0) issue_tile<8, 8, 1>(t, nv, lds_to, ln);
+                    else issue_tile<8, 8, 2>(t, nv, lds_to, ln);
+                } else {
+                    if (hf == 0) issue_tile<KB, VB, 1>(t, nv, lds_to, ln);
+                    else issue_tile<KB, VB, 2>(t, nv, lds_to, ln);
+                }
+            } else if (ring) {
+                if constexpr (SMALL) issue_q8_part<0>(t, nv, lds_to, ln);
+                else issue_tile<8, 8>(t, nv, lds_to, ln);
             } else {
-                issue_tile<KB, VB>(t, nv, st_lds, ln);
+                issue_tile<KB, VB>(t, nv, lds_to, ln);
             }
         };
 
         // physical page of tile i: the table is read only for sequences whose pages are not contiguous
         auto tile_page = [&](int i) {
-            const int p = c0 + ATP * (wv + AWAVES * i);
+            const int p = c0 + ATP * (sl + AWAVES * i);
             return sd.pbase >= 0 ? sd.pbase + __builtin_amdgcn_readfirstlane(p / spage) : page_of(S, seq, p);
         };
         int phys_cur = my > 0 ? tile_page(0) : 0; // page of the tile in the stage (tile i while step i runs)
@@ -644,34 +680,71 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SMALL ? 3 :
         if (a.kin) {
             const int pa = max(L - T, c0), pb = min(L, c1);
             for (int p = pa; p < pb; p++)
-                if (((p - c0) >> 5) % AWAVES == wv) new_tile0 = min(new_tile0, ((p - c0) >> 5) / AWAVES);
+                if (((p - c0) >> 5) % AWAVES == sl) new_tile0 = min(new_tile0, ((p - c0) >> 5) / AWAVES);
         }
         auto append_rows = [&]() {
             const int pa = max(L - T, c0), pb = min(L, c1);
             for (int p = pa; p < pb; p++) {
-                if (((p - c0) >> 5) % AWAVES != wv) continue;
+                if (((p - c0) >> 5) % AWAVES != sl) continue;
                 const size_t row = ((((size_t) si * T + (p - (L - T))) * a.kin_nl + l) * NKV + g) * HD;
 #pragma unroll
                 for (int w = 0; w < 2; w++) {
+                    if (WIDE && w != hf) continue; // (the pair's first wave stores K, the second V)
                     float v[4];
                     load_row4(w ? a.vin : a.kin, row, a.kin_f16, v);
                     store_row(S, w ? SV : SK, seq, g, p, true, v);
                 }
             }
         };
+        // ---- queries: FWHT when K is stored rotated, * 1/16, fp16 (qwen38_mk.cu:2873-2880), rows r = hh T + t.  The
+        // wave's rows are loaded before its first tile copy and waited for alone (loads return in order: vmcnt at most
+        // the copy count), so they are converted while tile 0 streams.  Only the copy issue runs between the loads and
+        // the wait (the loaded registers must not be read or moved before it).
         if (new_tile0 == 0) {
             append_rows();
             vm_wait<0>(); // the stored rows are in L2 before this wave's copies read them
         }
-        if (my > 0) issue(0, phys_cur);
-        if (new_tile0 > 0 && new_tile0 < my) append_rows(); // stored while the first tiles stream
-        // ---- queries: FWHT when K is stored rotated, * 1/16, fp16 (qwen38_mk.cu:2873-2880), rows r = hh T + t
-        for (int r = wv; r < RP; r += AWAVES) {
+        const int qrow0 = WIDE ? 0 : row0; // the workgroup's first row
+        constexpr int QPW = NQ / NW;       // rows per wave
+        f32x4 qx[QPW];
+#pragma unroll
+        for (int j = 0; j < QPW; j++) {
+            const int r = qrow0 + wv + NW * j;
+            if (r < a.R) {
+                const int hh = r / T, t = r % T;
+                qx[j] = gload16(a.q + (((size_t) (l * a.nseq + si) * T + t) * NH + GQA * g + hh) * a.qs + 4 * lane);
+            } else {
+                qx[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+            }
+        }
+        if (my > 0) {
+            issue(0, phys_cur, lds0 + stage_of(0) * SB);
+            // copy instructions of tile 0 (issue_tile / issue_q8_part): every load before them has returned
+            const bool ring = S.kvrc > 0 && c0 + ATP * sl >= ws;
+            if constexpr (WIDE) {
+                if (hf == 0) {
+                    if (ring) vm_wait<8 + 1>();
+                    else vm_wait<KB + 1>();
+                } else {
+                    if (ring) vm_wait<8 + 1>();
+                    else vm_wait<VB + 1>();
+                }
+            } else if (ring) {
+                vm_wait<SMALL ? 8 + 1 : 8 + 8 + 1>();
+            } else {
+                vm_wait<KB + VB + 1>();
+            }
+        } else {
+            vm_wait<0>();
+        }
+#pragma unroll
+        for (int j = 0; j < QPW; j++) {
+            pin_after(qx[j]);
+            const int r = wv + NW * j, gr = qrow0 + r;
             half2v o0 = {(_Float16) 0.f, (_Float16) 0.f}, o1 = o0;
-            if (row0 + r < a.R) {
-                const int hh = (row0 + r) / T, t = (row0 + r) % T;
-                const float4 x = *reinterpret_cast<const float4 *>(a.q + (((size_t) (l * a.nseq + si) * T + t) * NH + GQA * g + hh) * a.qs + 4 * lane);
-                float v[4] = {x.x, x.y, x.z, x.w};
+            if (gr < a.R) {
+                const int t = gr % T;
+                float v[4] = {qx[j][0], qx[j][1], qx[j][2], qx[j][3]};
                 if (a.qnw) qk_prep(v, a.qnw + (size_t) l * HD, a.rope + (size_t) (L - T + t) * 32);
                 if ((a.krot >> (a.layer0 + l)) & 1u) fwht256_w64(v);
                 o0[0] = (_Float16) (v[0] * 0.0625f);
@@ -679,8 +752,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SMALL ? 3 :
                 o1[0] = (_Float16) (v[2] * 0.0625f);
                 o1[1] = (_Float16) (v[3] * 0.0625f);
             }
-            reinterpret_cast<uint2 *>(sQ + qchunk(r, lane >> 1))[lane & 1] = make_uint2(as_u(o0), as_u(o1));
+            reinterpret_cast<uint2 *>(sQ + (r / RP) * RP * (HD / 8) + qchunk(r % RP, lane >> 1))[lane & 1] = make_uint2(as_u(o0), as_u(o1));
         }
+        if (new_tile0 > 0 && new_tile0 < my) append_rows(); // stored while the first tiles stream
         WaveState<NP> st;
 #pragma unroll
         for (int h = 0; h < NP; h++) {
@@ -695,7 +769,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SMALL ? 3 :
         __syncthreads(); // the query rows are complete
         if constexpr (NP == 1) {
 #pragma unroll
-            for (int ks = 0; ks < 8; ks++) st.qf[ks] = sQ[qchunk(n >> 1, 8 * q + ks)];
+            for (int ks = 0; ks < 8; ks++) st.qf[ks] = sQh[qchunk(n >> 1, 8 * q + ks)];
         }
         const uint8_t * const stp = smem + wv * SB; // (derived from smem: LDS reads)
         // one tile: operands into registers, then the stage is free and the next tile streams in during the math
@@ -705,7 +779,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SMALL ? 3 :
             const int phys_next = i + 1 < my ? tile_page(i + 1) : 0; // the scalar load overlaps the wait below
             vm_wait<0>(); // tile i has landed (the wave's only copies in flight)
             RawTile<K2, V2> raw;
-            const int p0 = c0 + ATP * (wv + AWAVES * i);
+            const int p0 = c0 + ATP * (sl + AWAVES * i);
             if constexpr (SMALL && K2 == 8 && V2 == 8) { // a q8 window tile in two halves
                 const uint16_t * const sc = reinterpret_cast<const uint16_t *>(stp + 8192);
                 read_k<8, 8>(raw, stp, sc, n, q);
@@ -723,21 +797,38 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SMALL ? 3 :
                         read_v<8, 8>(r, stp, sc + 8 * ATP, tn, tq);
                     },
                     [&]() {
-                        if (i + 1 < my) issue(i + 1, phys_next);
+                        if (i + 1 < my) issue(i + 1, phys_next, st_lds);
                     });
             } else if constexpr (LATE_V) {
                 read_k<K2, V2>(raw, stp, n, q);
                 compute_tile<NP, K2, V2, true>(
                     st, sQ, p0, raw, [&](RawTile<K2, V2> & r, int tn, int tq) { read_v<K2, V2>(r, stp, tn, tq); },
                     [&]() {
-                        if (i + 1 < my) issue(i + 1, phys_next);
+                        if (i + 1 < my) issue(i + 1, phys_next, st_lds);
                     });
             } else {
                 read_k<K2, V2>(raw, stp, n, q);
                 read_v<K2, V2>(raw, stp, n, q);
                 lds_drain();
-                if (i + 1 < my) issue(i + 1, phys_next);
+                if (i + 1 < my) issue(i + 1, phys_next, st_lds);
                 compute_tile<NP, K2, V2>(st, sQ, p0, raw);
+            }
+            phys_cur = phys_next;
+        };
+        // WIDE: one workgroup barrier per step; tile i + 1 streams into the slice's other stage during tile i's math
+        auto wstep = [&](auto fmt, int i) {
+            constexpr int K2 = decltype(fmt)::kb, V2 = decltype(fmt)::vb;
+            set_prio(my - i);
+            const int phys_next = i + 1 < my ? tile_page(i + 1) : 0;
+            vm_wait<0>();    // this wave's half of tile i has landed
+            __syncthreads(); // both halves of every slice's tile i are staged; every wave is done with tile i - 1
+            if (i + 1 < my) issue(i + 1, phys_next, lds0 + stage_of((i + 1) & 1) * SB);
+            if (i < my) {
+                const uint8_t * const sp = smem + stage_of(i & 1) * SB;
+                RawTile<K2, V2> raw;
+                read_k<K2, V2>(raw, sp, n, q);
+                compute_tile<NP, K2, V2, true>(st, sQh, c0 + ATP * (sl + AWAVES * i), raw,
+                                               [&](RawTile<K2, V2> & r, int tn, int tq) { read_v<K2, V2>(r, sp, tn, tq); });
             }
             phys_cur = phys_next;
         };
@@ -745,20 +836,25 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SMALL ? 3 :
         // keep a single tile body live per loop (one body holding both formats costs registers)
         int i_ring = my;
         if (S.kvrc > 0) {
-            const int d = ws - c0 - ATP * wv;
+            const int d = ws - c0 - ATP * sl;
             i_ring = d <= 0 ? 0 : min(my, (d + AWAVES * ATP - 1) / (AWAVES * ATP));
         }
         int i = 0;
-        for (; i < i_ring; i++) step(Fmt<KB, VB>(), i);
-        for (; i < my; i++) step(Fmt<8, 8>(), i);
-        // ---- merge the 4 waves in order: M = max m_w, O = sum e_w O_w, l = sum e_w l_w.  Per pass of 16 rows (two
-        // groups) every wave writes its scaled O rows to its own LDS buffer (the stages are free), then each thread
-        // adds the 4 buffers in wave order.
-        constexpr int OLD = HD + 4;                                                   // row stride (floats) of a buffer
-        constexpr int MR = NP == 1 ? 8 : 16;                                          // rows per wave buffer
-        float * const s_m = reinterpret_cast<float *>(smem + AWAVES * MR * OLD * 4); // [AWAVES][RP]
-        float * const s_l = s_m + AWAVES * RP;                                        // [AWAVES][RP]
-        static_assert(AWAVES * MR * OLD * 4 + 2 * AWAVES * RP * 4 <= SLDS, "merge buffers inside the stages");
+        if constexpr (WIDE) { // every wave takes part in the my0 barriers
+            for (; i < i_ring; i++) wstep(Fmt<KB, VB>(), i);
+            for (; i < my0; i++) wstep(Fmt<8, 8>(), i);
+        } else {
+            for (; i < i_ring; i++) step(Fmt<KB, VB>(), i);
+            for (; i < my; i++) step(Fmt<8, 8>(), i);
+        }
+        // ---- merge the 4 waves (slices) of each row in order: M = max m_w, O = sum e_w O_w, l = sum e_w l_w.  Per pass
+        // of 16 rows (two groups) every wave writes its scaled O rows to its own LDS buffer (the stages are free), then
+        // each thread adds the 4 buffers of its rows' waves in slice order.
+        constexpr int OLD = HD + 4;                                           // row stride (floats) of a buffer
+        constexpr int MR = NP == 1 ? 8 : 16;                                  // rows per wave buffer
+        float * const s_m = reinterpret_cast<float *>(smem + NW * MR * OLD * 4); // [NW][RP]
+        float * const s_l = s_m + NW * RP;                                    // [NW][RP]
+        static_assert(NW * MR * OLD * 4 + 2 * NW * RP * 4 <= SLDS, "merge buffers inside the stages");
         __syncthreads(); // every wave is done with its stage
         if (q == 0 && !(n & 1)) {
 #pragma unroll
@@ -768,7 +864,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SMALL ? 3 :
             }
         }
         __syncthreads();
-        const int R = a.R, RB = min(RP, R - row0); // rows of this batch
+        const int R = a.R;
+        // the merging thread's half (WIDE: threads 256 h .. 256 h + 255 add the buffers of waves 4 h .. 4 h + 3)
+        const int th = WIDE ? threadIdx.x / 256 : 0, tl = threadIdx.x - 256 * th, wb = AWAVES * th;
+        const int trow0 = WIDE ? RP * th : row0, RB = min(RP, R - trow0); // its rows
+        const float * const s_mh = s_m + wb * RP, * const s_mw = s_m + hf * AWAVES * RP; // the thread's / the wave's half
         constexpr int NPASS = (NP + 1) / 2;
 #pragma unroll
         for (int ps = 0; ps < NPASS; ps++) {
@@ -777,7 +877,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SMALL ? 3 :
                 const int h = 2 * ps + hh;
                 if (h < NP) {
                     const int row = 8 * h + (n >> 1);
-                    const float M = fmaxf(fmaxf(s_m[row], s_m[RP + row]), fmaxf(s_m[2 * RP + row], s_m[3 * RP + row]));
+                    const float M = fmaxf(fmaxf(s_mw[row], s_mw[RP + row]), fmaxf(s_mw[2 * RP + row], s_mw[3 * RP + row]));
                     const float e = st.m[h] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(st.m[h] - M);
                     float * o = reinterpret_cast<float *>(smem) + (wv * MR + 8 * hh + (n >> 1)) * OLD + 64 * q + (n & 1);
 #pragma unroll
@@ -788,9 +888,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SMALL ? 3 :
             }
             __syncthreads();
             const int nrow = min(16, RB - 16 * ps);
-            for (int idx = threadIdx.x; idx < nrow * (HD / 4); idx += 256) {
+            for (int idx = tl; idx < nrow * (HD / 4); idx += 256) {
                 const int r16 = idx / (HD / 4), c4 = idx % (HD / 4);
-                const float * src = reinterpret_cast<const float *>(smem) + r16 * OLD + 4 * c4;
+                const float * src = reinterpret_cast<const float *>(smem) + (wb * MR + r16) * OLD + 4 * c4;
                 float4 y = *reinterpret_cast<const float4 *>(src);
 #pragma unroll
                 for (int w = 1; w < AWAVES; w++) {
@@ -800,20 +900,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SMALL ? 3 :
                     y.z += z.z;
                     y.w += z.w;
                 }
-                *reinterpret_cast<float4 *>(a.part + ((size_t) item * R + row0 + 16 * ps + r16) * HD + 4 * c4) = y;
+                *reinterpret_cast<float4 *>(a.part + ((size_t) item * R + trow0 + 16 * ps + r16) * HD + 4 * c4) = y;
             }
             if (ps + 1 < NPASS) __syncthreads();
         }
-        if (threadIdx.x < RB) {
-            const int row = threadIdx.x;
-            const float M = fmaxf(fmaxf(s_m[row], s_m[RP + row]), fmaxf(s_m[2 * RP + row], s_m[3 * RP + row]));
+        if (tl < RB) {
+            const int row = tl;
+            const float M = fmaxf(fmaxf(s_mh[row], s_mh[RP + row]), fmaxf(s_mh[2 * RP + row], s_mh[3 * RP + row]));
             float lsum = 0.f;
 #pragma unroll
             for (int w = 0; w < AWAVES; w++) {
-                const float ew = s_m[w * RP + row] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(s_m[w * RP + row] - M);
-                lsum += ew * s_l[w * RP + row];
+                const float ew = s_mh[w * RP + row] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(s_mh[w * RP + row] - M);
+                lsum += ew * s_l[(wb + w) * RP + row];
             }
-            a.ml[(size_t) item * R + row0 + row] = make_float2(M, lsum);
+            a.ml[(size_t) item * R + trow0 + row] = make_float2(M, lsum);
         }
         __syncthreads(); // the LDS is reused by the next item
     }
@@ -1344,15 +1444,15 @@ __global__ __launch_bounds__(256) void k_prefill_combine(PrefillArgs a) {
 // ------------------------------------------------------------------------------------------------ dispatch
 typedef void (*AttnKernel)(AttnArgs);
 
-template <int NP>
+template <int NP, bool WIDE = false>
 static AttnKernel pick(int kb, int vb) {
 #define QKV_VB(K)                                                                                                      \
     switch (vb) {                                                                                                      \
-    case 4: return k_attn<NP, K, 4>;                                                                                   \
-    case 5: return k_attn<NP, K, 5>;                                                                                   \
-    case 6: return k_attn<NP, K, 6>;                                                                                   \
-    case 7: return k_attn<NP, K, 7>;                                                                                   \
-    case 8: return k_attn<NP, K, 8>;                                                                                   \
+    case 4: return k_attn<NP, K, 4, false, WIDE>;                                                                      \
+    case 5: return k_attn<NP, K, 5, false, WIDE>;                                                                      \
+    case 6: return k_attn<NP, K, 6, false, WIDE>;                                                                      \
+    case 7: return k_attn<NP, K, 7, false, WIDE>;                                                                      \
+    case 8: return k_attn<NP, K, 8, false, WIDE>;                                                                      \
     default: return nullptr;                                                                                           \
     }
     switch (kb) {
@@ -1412,13 +1512,13 @@ hipError_t launch_attn(const AttnArgs & a, int kb, int vb, int max_blocks, int o
     if (small) k = pick_small(kb, vb);
     else if (np == 1) k = pick<1>(kb, vb);
     else if (np == 2) k = pick<2>(kb, vb);
-    else if (np == 3) k = pick<3>(kb, vb);
+    else if (np == 3) k = a.wide ? pick<3, true>(kb, vb) : pick<3>(kb, vb);
     if (!k) return hipErrorInvalidValue;
     static thread_local const void * configured[128];
     static thread_local int n_configured = 0;
     bool done = false;
     for (int i = 0; i < n_configured; i++) done |= configured[i] == (const void *) k;
-    const int lds = (small ? AWAVES * (1024 * (kb + vb) + 1024) : ATTN_LDS) + a.RP * HD * 2;
+    const int lds = a.wide ? 2 * (ATTN_LDS + a.RP * HD * 2) : (small ? AWAVES * (1024 * (kb + vb) + 1024) : ATTN_LDS) + a.RP * HD * 2;
     if (!done) {
         const hipError_t e = hipFuncSetAttribute((const void *) k, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
         if (e != hipSuccess) return e;
@@ -1426,7 +1526,7 @@ hipError_t launch_attn(const AttnArgs & a, int kb, int vb, int max_blocks, int o
     }
     int blocks = a.n_items;
     if (max_blocks > 0 && blocks > max_blocks) blocks = max_blocks;
-    hipExtLaunchKernelGGL(k, dim3(blocks), dim3(256), lds, st, ev0, ev1, 0, a);
+    hipExtLaunchKernelGGL(k, dim3(blocks), dim3(a.wide ? 512 : 256), lds, st, ev0, ev1, 0, a);
     return hipGetLastError();
 }
 

@@ -256,6 +256,7 @@ class KVStore:
         return dict(zip(("calls", "attn_ms", "combine_ms", "append_ms"), list(out)))
 
     def config(self, key, value):
-        """Knobs that never change results: "max_blocks" (attention grid cap, 0 = none) and "occupancy" (decode
-        workgroups per CU for one-token calls on small packed formats: 0 = by launch size, 2 or 3)."""
+        """Knobs that never change results: "max_blocks" (attention grid cap, 0 = none), "occupancy" (decode
+        workgroups per CU for one-token calls on small packed formats: 0 = by launch size, 2 or 3) and "wide" (T >= 5:
+        1 = one pass of 8-wave workgroups, 0 = two 24-row passes)."""
         _check(lib().mk_kv_config(self.h, key.encode(), value))

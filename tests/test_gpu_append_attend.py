@@ -1,7 +1,7 @@
 """mk_kv_append_attend (the step's K/V rows stored inside the attention launch) against mk_kv_append followed by
 mk_kv_attend, through the C ABI: the same output bits, the same stored rows (digests), and the store keeps working
 afterwards.  Covers new rows in a wave's first tile, rows straddling a segment boundary (two workgroups store them),
-row batches (T = 8), several layers with different formats, paged sequences, and fp16 / fp32 inputs."""
+48 query rows (T = 8, the 8-wave kernel), several layers with different formats, paged sequences, and fp16 / fp32 inputs."""
 import numpy as np
 import pytest
 
@@ -20,7 +20,7 @@ def step_inputs(rng, nseq, T, nl):
 @pytest.mark.parametrize("spec,win,lens,T,nl,f16,page", [
     ("K*=5r,V*=6", 2048, [20000], 1, 1, True, 0),        # several tiles per wave, the new row in the last ring tile
     ("K*=5r,V*=6", 2048, [40], 1, 2, False, 0),          # a short context: the new row in a wave's first tile
-    ("", 0, [1027], 8, 1, True, 0),                      # T = 8 (two row batches), rows 1019..1026 straddle segment 1024
+    ("", 0, [1027], 8, 1, True, 0),                      # T = 8 (8-wave kernel), rows 1019..1026 straddle segment 1024
     ("K0=4r,V0=7r,K1=8,V1=5", 640, [3190], 3, 2, False, 0),
     ("K*=5r,V*=6", 1024, [2300, 700, 3100], 2, 1, True, 256),
 ])

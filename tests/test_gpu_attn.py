@@ -76,13 +76,30 @@ def test_rotated_v_and_mixed_layers(qkv, oracle, torch_gpu):
 @pytest.mark.parametrize("T", [2, 3, 5, 8])
 def test_t_invariance(qkv, oracle, torch_gpu, T):
     """Token t of a T-row call equals a 1-row call at context n+t+1 (bitwise; bench/dattn_bench.cu:1140-1160).
-    T = 2 runs the 16-row kernel, T = 3 one 24-row batch, T = 5 a full and a ragged 24-row batch, T = 8 two."""
+    T = 2 runs the 16-row kernel, T = 3 the 24-row one, T = 5 and 8 the 8-wave kernel (a full and a ragged half of 24
+    rows; two full halves)."""
     torch = torch_gpu
     L = 3190
     st, out, (K, V, Q) = check_case(qkv, oracle, torch, "K*=5r,V*=6", 1024, L, T, seed=9 + T)
     for t in range(T):
         o1 = run_attend(torch, st, Q[:, :, t:t + 1], [0], [L - T + t + 1], 1)
         assert np.array_equal(o1[:, :, 0], out[:, :, t]), t
+
+
+@pytest.mark.parametrize("spec,win,L,T", [("K*=5r,V*=6", 2048, 20000, 8), ("", 0, 9001, 5), ("K*=4,V*=7r", 640, 17001, 6),
+                                          ("K0=8,V0=8,K1=6r,V1=5", 1024, 3190, 8)])
+def test_wide_equals_batched(qkv, oracle, torch_gpu, spec, win, L, T):
+    """T >= 5 (25..48 rows per kv head): the one-pass 8-wave kernel gives the bits of two 24-row batches, with
+    several tiles per wave, window tiles, a partial last tile, two layers and a capped grid."""
+    torch = torch_gpu
+    print(f"wide {spec} L={L} T={T}", flush=True)
+    st, out, (K, V, Q) = check_case(qkv, oracle, torch, spec, win, L, T, nl=2, seed=13 + T, outliers=True, layers_checked=[1])
+    st.config("wide", 0)
+    assert np.array_equal(run_attend(torch, st, Q, [0], [L], T), out)
+    st.config("wide", 1)
+    st.config("max_blocks", 37)
+    assert np.array_equal(run_attend(torch, st, Q, [0], [L], T), out)
+    st.config("max_blocks", 0)
 
 
 def test_grid_invariance(qkv, oracle, torch_gpu):

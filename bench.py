@@ -194,23 +194,33 @@ def bench_cfg2(torch, qkv, nsteps=512):
     torch.cuda.synchronize()
     t = (time.perf_counter() - t0) / nsteps
     prof = profiled(torch, st, run, 1)
-    side = torch.cuda.Stream()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.stream(side):
-        run(side.cuda_stream)  # warm on the capture stream
-        side.synchronize()
-        with torch.cuda.graph(graph, stream=side):
-            run(torch.cuda.current_stream().cuda_stream)
-    graph.replay()
-    torch.cuda.synchronize()
-    reps = 5
-    t0 = time.perf_counter()
-    for _ in range(reps):
+
+    def graph_us(fn):
+        """fn(stream) captured once as a HIP graph, replayed 5 times: wall-clock µs per step."""
+        side = torch.cuda.Stream()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(side):
+            fn(side.cuda_stream)  # warm on the capture stream
+            side.synchronize()
+            with torch.cuda.graph(graph, stream=side):
+                fn(torch.cuda.current_stream().cuda_stream)
         graph.replay()
-    torch.cuda.synchronize()
-    tg = (time.perf_counter() - t0) / (reps * nsteps)
+        torch.cuda.synchronize()
+        reps = 5
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            graph.replay()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / (reps * nsteps) * 1e6
+
+    tg = graph_us(run) * 1e-6
+    # the dispatch floor of one graph node (a one-element add), and the steps with cache-resident input rows
+    one = torch.zeros(1, device="cuda")
+    floor_us = graph_us(lambda stream: [one.add_(1) for _ in range(nsteps)])
+    hot_us = graph_us(lambda stream: [st.append(0, 0, nl, 8 * s, 8, kp, vp, 1, stream) for s in range(nsteps)])
     return {"steps": nsteps, "us_per_step": tg * 1e6, "graph_us_per_step": tg * 1e6, "eager_us_per_step": t * 1e6,
             "kernel_us_per_step": prof["append_ms"] / nsteps * 1e3, "rows_per_step": 8 * nl * NKV * 2,
+            "graph_node_floor_us": floor_us, "cache_resident_inputs_us_per_step": hot_us,
             "note": "us_per_step: the 512 steps captured once as a HIP graph and replayed (wall clock / 512); eager: one "
                     "library call per step from Python; kernel: per-launch events (which lengthen short launches)"}
 

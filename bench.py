@@ -139,6 +139,30 @@ def bench_cfg3(torch, qkv, steps, warmup):
 
     t_slot_sep = timed(torch, slot_separate, steps, warmup)
     t_slot_fused = timed(torch, slot_fused, steps, warmup)
+    # the slot with a stand-in for the layer's q/k/v projection before the attention (an fp16 GEMV of a 7,168 x 4,096
+    # weight, 58.7 MB, one per layer), without and with mk_kv_prefetch of the layer's first tiles on a second stream
+    # beside it; attention kernel times from the store's events
+    wts = torch.randn(nl, 7168, 4096, device="cuda", dtype=torch.float16, generator=g)
+    xin = torch.randn(4096, device="cuda", dtype=torch.float16, generator=g)
+    side = torch.cuda.Stream()
+
+    def slot_proj(prefetch):
+        main = torch.cuda.current_stream()
+        for l in range(nl):
+            if prefetch:
+                side.wait_stream(main)
+                st.prefetch(l, 1, [0], [L], 1, 1, side.cuda_stream)
+            torch.mv(wts[l], xin)
+            if prefetch:
+                main.wait_stream(side)
+            st.attend(l, 1, [0], [L], 1, qp + l * lay, op + l * lay)
+
+    proj = {}
+    for pf in (False, True):
+        t = timed(torch, lambda: slot_proj(pf), steps, warmup)
+        pp = profiled(torch, st, lambda: slot_proj(pf), steps)
+        proj["prefetch" if pf else "plain"] = {"step_s": t, "attn_kernel_avg_s": pp["attn_ms"] / pp["calls"] * 1e-3}
+    del wts
     ok = bool(torch.isfinite(out).all().item())
     return {
         "L": L, "ws": ws, "ring_positions": L - ws, "layers": nl,
@@ -149,7 +173,8 @@ def bench_cfg3(torch, qkv, steps, warmup):
         "fused16_step_s": t_fused, "fused16_positions_per_s": nl * L / t_fused,
         "fused16_gbps": nl * per_layer_bytes / t_fused / 1e9, "fused16_attn_kernel_avg_s": fused_attn_avg,
         "fused16_attn_kernel_gbps": nl * per_layer_bytes / fused_attn_avg / 1e9,
-        "slot_append_then_attend_step_s": t_slot_sep, "slot_append_attend_fused_step_s": t_slot_fused, "finite": ok,
+        "slot_append_then_attend_step_s": t_slot_sep, "slot_append_attend_fused_step_s": t_slot_fused,
+        "slot_after_projection": proj, "finite": ok,
     }
 
 

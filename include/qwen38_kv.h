@@ -68,6 +68,15 @@ int mk_kv_attend(void * h, int layer0, int n_layers, int n_seq, const int * seqs
                  void * stream);
 
 /*
+ * Prefetch for a later mk_kv_attend with the same (layer0, n_layers, seqs, lens, T): the first `tiles` (1..64) tiles
+ * of every wave slice of every work item are read by a launch with the attention's grid and work-item order, so they
+ * sit in the L2 of the XCD whose workgroup will stream them (and in the last-level cache).  Issue it on another
+ * stream beside independent work (the layer's projections) before the attention; it writes nothing.  Same checks as
+ * mk_kv_attend.  Replaces the L2 prefetch of the first KV lines in attn_proj (pf_l2, qwen38_mk.cu:2600-2621).
+ */
+int mk_kv_prefetch(void * h, int layer0, int n_layers, int n_seq, const int * seqs, const int * lens, int T, int tiles, void * stream);
+
+/*
  * mk_kv_append followed by mk_kv_attend in one launch: the T new rows of every sequence (positions lens[i] - T ..
  * lens[i] - 1; k, v device [n_seq][T][n_layers][4][256] of fp32 (dtype 0) or fp16 (dtype 1), rows after RMSNorm/RoPE)
  * are stored by the attention kernel itself -- by the wave whose tiles hold them, before those tiles are copied --

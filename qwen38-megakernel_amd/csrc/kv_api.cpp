@@ -480,9 +480,10 @@ static int append_impl(void * h, int seq, int layer0, int n_layers, int pos, int
 static int attend_impl(void * h, int layer0, int n_layers, int n_seq, const int * seqs, const int * lens, int T, const float * q,
                        int qs, const float * qnw, const float * gate, int gs, float * out, int8_t * q32a, int8_t * q32b, uint16_t * q32m,
                        void * stream, void * ws = nullptr, size_t ws_bytes = 0, const void * kin = nullptr, const void * vin = nullptr,
-                       int kdtype = 0) {
+                       int kdtype = 0, int prefetch_tiles = 0) {
     return guarded([&] {
         Store & s = *as_store(h);
+        const bool prefetch = prefetch_tiles > 0; // mk_kv_prefetch: the launch geometry only, no queries or outputs
         if ((kin != nullptr) != (vin != nullptr)) throw std::runtime_error("null K/V pointer");
         if (kin && kdtype != 0 && kdtype != 1) throw std::runtime_error("dtype: 0 fp32, 1 fp16");
         if ((q32a != nullptr) != (q32b != nullptr) || (q32a != nullptr) != (q32m != nullptr))
@@ -490,7 +491,7 @@ static int attend_impl(void * h, int layer0, int n_layers, int n_seq, const int 
         check_layers(s, layer0, n_layers);
         if (T < 1 || T > MAXT) throw std::runtime_error("T must be 1..8");
         if (n_seq < 1 || n_seq > MAX_SEQ) throw std::runtime_error("1..8 sequences per attend call");
-        if (!q || !out) throw std::runtime_error("null q/out pointer");
+        if (!prefetch && (!q || !out)) throw std::runtime_error("null q/out pointer");
         hipStream_t st = static_cast<hipStream_t>(stream);
         AttnArgs a{};
         a.S = s.S;
@@ -551,9 +552,10 @@ static int attend_impl(void * h, int layer0, int n_layers, int n_seq, const int 
         }
         const size_t max_items = (size_t) n_layers * NKV * seg_total;
         const size_t part_need = (max_items * a.R * HD * sizeof(float) + 255) / 256 * 256, ml_need = max_items * a.R * sizeof(float2);
-        float * part_base;
-        float2 * ml_base;
-        if (ws) {
+        float * part_base = nullptr;
+        float2 * ml_base = nullptr;
+        if (prefetch) {
+        } else if (ws) {
             if (part_need + ml_need > ws_bytes)
                 throw std::runtime_error("the call needs " + std::to_string(part_need + ml_need) + " bytes of attention workspace, more than the " +
                                          std::to_string(ws_bytes) + " available to an allocation-free call");
@@ -565,7 +567,7 @@ static int attend_impl(void * h, int layer0, int n_layers, int n_seq, const int 
             part_base = static_cast<float *>(s.part);
             ml_base = static_cast<float2 *>(s.ml);
         }
-        Store::EvSet * es = prof_set(s, 1);
+        Store::EvSet * es = prefetch ? nullptr : prof_set(s, 1); // (a prefetch is not timed)
         size_t item_base = 0;
         AttnArgs groups[MAX_LAYERS]; // at most one launch per layer (no host allocation on this path)
         size_t ng = 0;
@@ -585,8 +587,10 @@ static int attend_impl(void * h, int layer0, int n_layers, int n_seq, const int 
             }
             b.n_base = item;
             b.n_items = item * (a.wide ? 1 : (a.R + a.RP - 1) / a.RP);
-            b.q = q + (size_t) l * n_seq * T * NH * qs;
-            b.out = out + (size_t) l * n_seq * T * NH * HD;
+            if (!prefetch) {
+                b.q = q + (size_t) l * n_seq * T * NH * qs;
+                b.out = out + (size_t) l * n_seq * T * NH * HD;
+            }
             if (gate) b.gate = gate + (size_t) l * n_seq * T * NH * gs;
             if (qnw) b.qnw = qnw + (size_t) l * HD;
             if (kin) {
@@ -601,11 +605,18 @@ static int attend_impl(void * h, int layer0, int n_layers, int n_seq, const int 
                 b.q32b = q32b + (size_t) l * n_seq * T * 192 * 16;
                 b.q32m = q32m + (size_t) l * n_seq * T * 192 * 4;
             }
-            b.part = part_base + item_base * a.R * HD;
-            b.ml = ml_base + item_base * a.R;
+            if (!prefetch) {
+                b.part = part_base + item_base * a.R * HD;
+                b.ml = ml_base + item_base * a.R;
+            }
             item_base += (size_t) item;
             groups[ng++] = b;
             l = e;
+        }
+        if (prefetch) {
+            for (size_t g = 0; g < ng; g++)
+                HCK(launch_prefetch(groups[g], s.S.side[groups[g].layer0][0].bits, s.S.side[groups[g].layer0][1].bits, prefetch_tiles, st));
+            return 0;
         }
         // profiling: the first launch records the start event, the last the end event (kernel timestamps)
         auto ev = [&](int i, size_t g) { return es && ((i % 2 == 0 && g == 0) || (i % 2 == 1 && g + 1 == ng)) ? es->e[i] : nullptr; };
@@ -639,6 +650,15 @@ int mk_kv_append_prep(void * h, int seq, int layer0, int n_layers, int pos, int 
 int mk_kv_attend(void * h, int layer0, int n_layers, int n_seq, const int * seqs, const int * lens, int T, const float * q, float * out,
                  void * stream) {
     return attend_impl(h, layer0, n_layers, n_seq, seqs, lens, T, q, HD, nullptr, nullptr, HD, out, nullptr, nullptr, nullptr, stream);
+}
+
+int mk_kv_prefetch(void * h, int layer0, int n_layers, int n_seq, const int * seqs, const int * lens, int T, int tiles, void * stream) {
+    if (tiles < 1 || tiles > 64) {
+        g_err = "tiles must be 1..64";
+        return -1;
+    }
+    return attend_impl(h, layer0, n_layers, n_seq, seqs, lens, T, nullptr, HD, nullptr, nullptr, HD, nullptr, nullptr, nullptr, nullptr, stream,
+                       nullptr, 0, nullptr, nullptr, 0, tiles);
 }
 
 int mk_kv_append_attend(void * h, int layer0, int n_layers, int n_seq, const int * seqs, const int * lens, int T, const void * k, const void * v,

@@ -919,6 +919,41 @@ __global__ __launch_bounds__(WIDE ? 512 : 256) __attribute__((amdgpu_waves_per_e
     }
 }
 
+// ------------------------------------------------------------------------------------------------ prefetch
+// The first `tiles` tiles of every wave slice of an attention launch's work items copied into LDS and dropped: the
+// bytes pass through the L2 of the XCD that workgroup x runs on, and the attention launch with the same arguments puts
+// work item x on workgroup x -- the same XCD (workgroups go round-robin over the XCDs by index) -- so its first tile
+// copies hit that L2 (or the last-level cache) instead of HBM.  No results: issued ahead of the attention, on another
+// stream beside independent work (the reference's pf_l2 in attn_proj, qwen38_mk.cu:2600-2621).
+template <int KB, int VB>
+__global__ __launch_bounds__(256) void k_prefetch(AttnArgs a, int tiles) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const StoreLayout & S = a.S;
+    const unsigned st_lds = (unsigned) __builtin_amdgcn_readfirstlane((unsigned) (size_t) (__attribute__((address_space(3))) uint8_t *) smem + wv * STAGE_BYTES);
+    for (int item = blockIdx.x; item < a.n_items; item += gridDim.x) {
+        int si = 0;
+        for (int i = 1; i < a.nseq; i++)
+            if (item >= a.sd[i].item0) si = i;
+        const SeqDesc sd = a.sd[si];
+        const int local = item - sd.item0, seg = local % sd.nseg, lg = local / sd.nseg, g = lg % NKV, l = lg / NKV;
+        const int c0 = seg * sd.cs, c1 = min(sd.L, c0 + sd.cs), ntiles = (c1 - c0 + ATP - 1) / ATP;
+        const SideLayout SK = S.side[a.layer0 + l][0], SV = S.side[a.layer0 + l][1];
+        const size_t ring0 = (size_t) (sd.seq * NKV + g) * S.kvrc;
+        for (int i = 0; i < tiles; i++) {
+            const int tix = wv + AWAVES * i;
+            if (tix >= ntiles) break;
+            const int p0 = c0 + ATP * tix, nv = min(ATP, sd.L - p0);
+            const int phys = sd.pbase >= 0 ? sd.pbase + p0 / S.page : page_of(S, sd.seq, p0);
+            const bool ring = S.kvrc > 0 && p0 >= sd.ws;
+            const TileSrc t = tile_src<KB, VB>(S, SK, SV, g, p0, phys, ring0, ring);
+            if (ring) issue_tile<8, 8>(t, nv, st_lds, lane);
+            else issue_tile<KB, VB>(t, nv, st_lds, lane);
+            vm_wait<0>(); // (the stage is reused by the next copy)
+        }
+    }
+}
+
 // ------------------------------------------------------------------------------------------------ output epilogue
 // One output row y (head h of token row trow, lane l holding dims 4l .. 4l+3) after the merge: the V un-rotation when
 // V is stored rotated, the sigmoid output gate (qwen38_mk.cu:4686) when grow is given, the fp32 store, and when q32a
@@ -1571,6 +1606,41 @@ hipError_t launch_prefill(const PrefillArgs & a, int kb, int vb, hipStream_t st,
     if (e != hipSuccess) return e;
     hipExtLaunchKernelGGL(k_prefill_combine, dim3((a.R * NKV + 3) / 4), dim3(256), 0, st, nullptr, ev1, 0, a);
     return hipGetLastError();
+}
+
+
+template <int KB, int VB>
+static hipError_t prefetch_kb_vb(const AttnArgs & a, int tiles, hipStream_t st) {
+    constexpr int lds = ATTN_LDS;
+    static thread_local bool configured = false; // (per instantiation, as launch_attn does)
+    if (!configured) {
+        const hipError_t e = hipFuncSetAttribute((const void *) k_prefetch<KB, VB>, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+        if (e != hipSuccess) return e;
+        configured = true;
+    }
+    hipLaunchKernelGGL((k_prefetch<KB, VB>), dim3(a.n_items), dim3(256), lds, st, a, tiles);
+    return hipGetLastError();
+}
+
+hipError_t launch_prefetch(const AttnArgs & a, int kb, int vb, int tiles, hipStream_t st) {
+#define QKV_VB(K)                                                                                                      \
+    switch (vb) {                                                                                                      \
+    case 4: return prefetch_kb_vb<K, 4>(a, tiles, st);                                                                 \
+    case 5: return prefetch_kb_vb<K, 5>(a, tiles, st);                                                                 \
+    case 6: return prefetch_kb_vb<K, 6>(a, tiles, st);                                                                 \
+    case 7: return prefetch_kb_vb<K, 7>(a, tiles, st);                                                                 \
+    case 8: return prefetch_kb_vb<K, 8>(a, tiles, st);                                                                 \
+    default: return hipErrorInvalidValue;                                                                              \
+    }
+    switch (kb) {
+    case 4: QKV_VB(4)
+    case 5: QKV_VB(5)
+    case 6: QKV_VB(6)
+    case 7: QKV_VB(7)
+    case 8: QKV_VB(8)
+    default: return hipErrorInvalidValue;
+    }
+#undef QKV_VB
 }
 
 } // namespace qkv

@@ -103,6 +103,8 @@ hipError_t launch_ring_refill(const StoreLayout & S, int seq, int nl, int p0, in
 // work items than two per CU hold, else two; 2 = two; 3 = three
 hipError_t launch_attn(const AttnArgs & a, int kb, int vb, int max_blocks, int occ, hipStream_t st, hipEvent_t ev0 = nullptr,
                        hipEvent_t ev1 = nullptr);
+// the first `tiles` tiles of every wave slice of the attention launch `a` read into the L2 its workgroups will use
+hipError_t launch_prefetch(const AttnArgs & a, int kb, int vb, int tiles, hipStream_t st);
 hipError_t launch_combine(const AttnArgs & a, hipStream_t st, hipEvent_t ev0 = nullptr, hipEvent_t ev1 = nullptr);
 hipError_t launch_prefill(const PrefillArgs & a, int kb, int vb, hipStream_t st, hipEvent_t ev0 = nullptr, hipEvent_t ev1 = nullptr);
 

@@ -27,6 +27,7 @@ SIGNATURES = {
     "mk_kv_set_pages": (_c_int, [_c_vp, _c_int, _P_int, _c_int]),
     "mk_kv_append": (_c_int, [_c_vp, _c_int, _c_int, _c_int, _c_int, _c_int, _c_vp, _c_vp, _c_int, _c_vp]),
     "mk_kv_attend": (_c_int, [_c_vp, _c_int, _c_int, _c_int, _P_int, _P_int, _c_int, _c_vp, _c_vp, _c_vp]),
+    "mk_kv_prefetch": (_c_int, [_c_vp, _c_int, _c_int, _c_int, _P_int, _P_int, _c_int, _c_int, _c_vp]),
     "mk_kv_append_attend": (_c_int, [_c_vp, _c_int, _c_int, _c_int, _P_int, _P_int, _c_int, _c_vp, _c_vp, _c_int, _c_vp, _c_vp, _c_vp]),
     "mk_kv_attend_noalloc": (_c_int, [_c_vp, _c_int, _c_int, _c_int, _P_int, _P_int, _c_int, _c_vp, _c_vp, _c_vp]),
     "mk_kv_attend_gated": (_c_int, [_c_vp, _c_int, _c_int, _c_int, _P_int, _P_int, _c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _P_u16,
@@ -157,6 +158,13 @@ class KVStore:
         s = (ctypes.c_int * n)(*seqs)
         l = (ctypes.c_int * n)(*lens)
         _check(lib().mk_kv_append_attend(self.h, layer0, n_layers, n, s, l, T, k_ptr, v_ptr, dtype, q_ptr, out_ptr, stream))
+
+    def prefetch(self, layer0, n_layers, seqs, lens, T, tiles=1, stream=0):
+        """read the first `tiles` tiles of each wave slice of a later attend into the L2 its workgroups use."""
+        n = len(seqs)
+        s = (ctypes.c_int * n)(*seqs)
+        l = (ctypes.c_int * n)(*lens)
+        _check(lib().mk_kv_prefetch(self.h, layer0, n_layers, n, s, l, T, tiles, stream))
 
     def attend_noalloc(self, layer0, n_layers, seqs, lens, T, q_ptr, out_ptr, stream=0):
         """attend with the partials in the library's per-device array (mk_kv_attend_noalloc): allocates nothing."""

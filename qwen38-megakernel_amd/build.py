@@ -13,7 +13,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libqwen38_kv.so")
-SOURCES = ["kv_store.hip", "kv_attn.hip", "kv_api.cpp"]
+SOURCES = ["kv_store.hip", "kv_attn.hip", "kv_attn_fused.hip", "kv_api.cpp"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [

@@ -195,14 +195,23 @@ __device__ __forceinline__ unsigned quant_qn(const float (&v)[4], int bits, uint
 // One row per wave: lane l holds values 4l .. 4l+3 (kv_store, qwen38_mk.cu:2099-2116).  Used by the append kernel and
 // by the attention kernel's fused append (mk_kv_append_attend), so both store the same bytes.
 
-__device__ __forceinline__ size_t main_row(const StoreLayout & S, int seq, int g, int p) {
+// the store geometry a row's addresses need (the part of StoreLayout a called function takes as plain values)
+struct RowGeo {
+    const int * ptab;
+    int pt_stride, page, n_pages, kvrc;
+};
+__device__ __forceinline__ RowGeo geo_of(const StoreLayout & S) { return RowGeo{S.ptab, S.pt_stride, S.page, S.n_pages, S.kvrc}; }
+
+__device__ __forceinline__ size_t main_row(const RowGeo & S, int seq, int g, int p) {
     const int lp = p / S.page;
     const int phys = S.ptab[seq * S.pt_stride + lp];
     return (size_t) (g * S.n_pages + phys) * S.page + (p - lp * S.page);
 }
-__device__ __forceinline__ size_t ring_row(const StoreLayout & S, int seq, int g, int p) {
+__device__ __forceinline__ size_t main_row(const StoreLayout & S, int seq, int g, int p) { return main_row(geo_of(S), seq, g, p); }
+__device__ __forceinline__ size_t ring_row(const RowGeo & S, int seq, int g, int p) {
     return (size_t) (seq * NKV + g) * S.kvrc + p % S.kvrc;
 }
+__device__ __forceinline__ size_t ring_row(const StoreLayout & S, int seq, int g, int p) { return ring_row(geo_of(S), seq, g, p); }
 
 // the lane's 4 values of input row `row` (elements row .. row + 255) of fp16 (f16) or fp32 data
 __device__ __forceinline__ void load_row4(const void * in, size_t row, int f16, float (&v)[4]) {
@@ -225,7 +234,7 @@ __device__ __forceinline__ void load_row4(const void * in, size_t row, int f16, 
 
 // the row of position p (kv head g of sequence seq) on side sd: optional FWHT, the main row in the side's format and,
 // when ring and the side has a window, the q8 ring copy of the same rotated values.  All 64 lanes call it.
-__device__ __forceinline__ void store_row(const StoreLayout & S, const SideLayout & sd, int seq, int g, int p, bool ring, float (&v)[4]) {
+__device__ __forceinline__ void store_row(const RowGeo & S, const SideLayout & sd, int seq, int g, int p, bool ring, float (&v)[4]) {
     const int lane = lane_id();
     if (sd.rot) fwht256_w64(v);
     const size_t row = main_row(S, seq, g, p);
@@ -259,6 +268,10 @@ __device__ __forceinline__ void store_row(const StoreLayout & S, const SideLayou
         *reinterpret_cast<unsigned *>(sd.ring + rr * HD + 4 * lane) = word;
         if ((lane & 7) == 0) sd.rsc[rr * 8 + (lane >> 3)] = rs;
     }
+}
+
+__device__ __forceinline__ void store_row(const StoreLayout & S, const SideLayout & sd, int seq, int g, int p, bool ring, float (&v)[4]) {
+    store_row(geo_of(S), sd, seq, g, p, ring, v);
 }
 
 // ------------------------------------------------------------------------------------------------ dequantization

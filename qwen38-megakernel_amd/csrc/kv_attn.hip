@@ -563,15 +563,15 @@ __global__ __launch_bounds__(256) void k_prefill_combine(PrefillArgs a) {
 
 // ------------------------------------------------------------------------------------------------ dispatch
 
-template <int NP, bool WIDE = false>
+template <int NP>
 static AttnKernel pick(int kb, int vb) {
 #define QKV_VB(K)                                                                                                      \
     switch (vb) {                                                                                                      \
-    case 4: return k_attn<NP, K, 4, false, WIDE>;                                                                      \
-    case 5: return k_attn<NP, K, 5, false, WIDE>;                                                                      \
-    case 6: return k_attn<NP, K, 6, false, WIDE>;                                                                      \
-    case 7: return k_attn<NP, K, 7, false, WIDE>;                                                                      \
-    case 8: return k_attn<NP, K, 8, false, WIDE>;                                                                      \
+    case 4: return k_attn<NP, K, 4>;                                                                                   \
+    case 5: return k_attn<NP, K, 5>;                                                                                   \
+    case 6: return k_attn<NP, K, 6>;                                                                                   \
+    case 7: return k_attn<NP, K, 7>;                                                                                   \
+    case 8: return k_attn<NP, K, 8>;                                                                                   \
     default: return nullptr;                                                                                           \
     }
     switch (kb) {
@@ -633,7 +633,7 @@ hipError_t launch_attn(const AttnArgs & a, int kb, int vb, int max_blocks, int o
     else if (small) k = pick_small(kb, vb);
     else if (np == 1) k = pick<1>(kb, vb);
     else if (np == 2) k = pick<2>(kb, vb);
-    else if (np == 3) k = a.wide ? pick<3, true>(kb, vb) : pick<3>(kb, vb);
+    else if (np == 3) k = a.wide ? verify_of<false>(kb, vb) : pick<3>(kb, vb);
     if (!k) return hipErrorInvalidValue;
     static thread_local const void * configured[256];
     static thread_local int n_configured = 0;
@@ -646,6 +646,7 @@ hipError_t launch_attn(const AttnArgs & a, int kb, int vb, int max_blocks, int o
         if (n_configured < 256) configured[n_configured++] = (const void *) k;
     }
     int blocks = a.n_items;
+    if (a.wide) blocks = std::min(blocks, device_cus()); // k_verify: persistent, one workgroup per CU
     if (max_blocks > 0 && blocks > max_blocks) blocks = max_blocks;
     hipExtLaunchKernelGGL(k, dim3(blocks), dim3(a.wide ? 512 : 256), lds, st, ev0, ev1, 0, a);
     return hipGetLastError();

@@ -601,23 +601,17 @@ __device__ __forceinline__ void set_prio(int left) {
 
 // ------------------------------------------------------------------------------------------------ the kernel
 // More than 16 query rows (T >= 3) are held as 24 rows per wave (three groups; 48 rows of accumulators in one wave
-// spill).  T = 3, 4: one 24-row pass.  T = 5..8: the WIDE kernel below, or (knob) batches of 24 rows: work item =
-// (sequence, layer, kv head, segment, row batch), batch-minor, each batch streaming the segment's tiles again.  Every
-// row sees the same slices, tile arithmetic and merge whatever T and whichever kernel.
-// WIDE (25..48 rows, T = 5..8): one pass instead of two batches.  8 waves: waves w and w + 4 take the same slice of
-// tiles (w, w + 4, ..) for rows 0..23 and 24..47, and share two stages per slice: at step i (after a workgroup barrier)
-// tile i + 1 is copied into the other stage -- the K rows by the first wave of the pair, the V rows by the second --
-// while both compute tile i.  A row's slices, tile arithmetic and merge order are those of the batched kernel.
+// spill).  T = 3, 4: one 24-row pass.  T = 5..8: k_verify below (one pass, 8 waves), or (knob) batches of 24 rows
+// here: work item = (sequence, layer, kv head, segment, row batch), batch-minor, each batch streaming the segment's
+// tiles again.  Every row sees the same slices, tile arithmetic and merge whatever T and whichever kernel.
 // SMALL (one 8-row group, KB + VB <= 11): three workgroups per CU for launches with many work items.  The stages hold
 // one packed tile (32 (KB + VB) + 1 KiB); a q8 window tile goes through in two halves (issue_q8_part); the V operands
 // are read after the scores (168 registers).  Same slices and arithmetic: bitwise the same partials.
-template <int NP, int KB, int VB, bool SMALL = false, bool WIDE = false, bool APPEND = false>
-__global__ __launch_bounds__(WIDE ? 512 : 256) __attribute__((amdgpu_waves_per_eu(SMALL ? 3 : 2, SMALL ? 3 : 2))) void k_attn(AttnArgs a) {
+template <int NP, int KB, int VB, bool SMALL = false, bool APPEND = false>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SMALL ? 3 : 2, SMALL ? 3 : 2))) void k_attn(AttnArgs a) {
     static_assert(!SMALL || (NP == 1 && KB + VB <= 11), "small stages: one row group, packed tiles of at most 11 KiB");
-    static_assert(!WIDE || NP == 3, "wide: two halves of 24 rows");
-    constexpr int RP = 8 * NP;                // query rows held by a wave (the padding rows are zero)
-    constexpr int NW = WIDE ? 2 * AWAVES : AWAVES, NQ = WIDE ? 2 * RP : RP; // waves, query rows of the workgroup
-    constexpr int SB = SMALL ? 1024 * (KB + VB) + 1024 : STAGE_BYTES, SLDS = NW * SB; // stage bytes, all stages
+    constexpr int RP = 8 * NP; // query rows held (the padding rows are zero)
+    constexpr int SB = SMALL ? 1024 * (KB + VB) + 1024 : STAGE_BYTES, SLDS = AWAVES * SB; // stage bytes, all stages
     // NP = 3: the V operands are read from the stage after the scores (the stage is refilled only then), so a wave
     // never holds a whole raw tile in registers next to 24 rows of accumulators, and two workgroups fit a CU
     constexpr bool LATE_V = NP >= 3 || SMALL;
@@ -625,14 +619,11 @@ __global__ __launch_bounds__(WIDE ? 512 : 256) __attribute__((amdgpu_waves_per_e
     // the wave index as a scalar: tile positions, page lookups and source selection stay scalar (SMEM loads, uniform
     // branches); vector loads there would need vmcnt waits that also drain the tile copies in flight
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63, n = lane & 15, q = lane >> 4;
-    const int sl = WIDE ? wv & (AWAVES - 1) : wv, hf = WIDE ? wv / AWAVES : 0; // the wave's slice of tiles, row half
+    const int sl = wv; // the wave's slice of tiles: w, w + 4, ..
     const StoreLayout & S = a.S;
     const unsigned lds0 = (unsigned) (size_t) (__attribute__((address_space(3))) uint8_t *) smem;
-    // stage b (0, 1) of the wave's slice: one per wave, or two per slice (WIDE)
-    auto stage_of = [&](int b) { return WIDE ? 2 * sl + b : wv; };
     const unsigned st_lds = (unsigned) __builtin_amdgcn_readfirstlane(lds0 + wv * SB);
-    half8 * const sQ = reinterpret_cast<half8 *>(smem + SLDS); // [NQ][256] fp16, chunk-swizzled (qchunk) per half
-    const half8 * const sQh = sQ + hf * RP * (HD / 8);          // the wave's rows
+    half8 * const sQ = reinterpret_cast<half8 *>(smem + SLDS); // [RP][256] fp16, chunk-swizzled (qchunk)
     // The first tile copy of an item waits on every scalar load before it, and each round trip to the kernel arguments
     // costs a few hundred ns at launch: the common case (one sequence, one layer) needs one round -- the header, sd[0]
     // and side0 at fixed offsets, made live together by the empty asm so that the loads issue back to back and are
@@ -645,7 +636,7 @@ __global__ __launch_bounds__(WIDE ? 512 : 256) __attribute__((amdgpu_waves_per_e
                  "s"(V0.scs), "s"(V0.ring), "s"(V0.rsc), "s"(a.T), "s"(a.R), "s"(a.layer0), "s"(a.krot), "s"(a.qs), "s"(a.q),
                  "s"(a.qnw), "s"(a.rope), "s"(S.ptab), "s"(S.pt_stride));
     for (int bitem = blockIdx.x; bitem < n_items; bitem += gridDim.x) {
-        const int nb = n_items / n_base, item = bitem / nb, batch = bitem - item * nb, row0 = RP * (WIDE ? hf : batch);
+        const int nb = n_items / n_base, item = bitem / nb, batch = bitem - item * nb, row0 = RP * batch;
         int si = 0;
         SeqDesc sd = sd0;
         if (nseq > 1) {
@@ -664,7 +655,6 @@ __global__ __launch_bounds__(WIDE ? 512 : 256) __attribute__((amdgpu_waves_per_e
         const int c0 = seg * sd.cs, c1 = min(L, c0 + sd.cs);
         const int ntiles = (c1 - c0 + ATP - 1) / ATP;
         const int my = ntiles > sl ? (ntiles - sl + AWAVES - 1) / AWAVES : 0; // tiles sl, sl+4, ..
-        const int my0 = (ntiles + AWAVES - 1) / AWAVES;                       // steps of the workgroup (slice 0)
         SideLayout SK = K0, SV = V0;
         if (l > 0) {
             SK = S.side[a.layer0 + l][0];
@@ -679,15 +669,7 @@ __global__ __launch_bounds__(WIDE ? 512 : 256) __attribute__((amdgpu_waves_per_e
             const TileSrc t = tile_src<KB, VB>(S, SK, SV, g, p0, phys, ring0, ring);
             int ln = lane; // opaque: the per-lane chunk addresses are not hoisted out of the tile loop into registers
             asm volatile("" : "+v"(ln));
-            if constexpr (WIDE) {
-                if (ring) {
-                    if (hf == 0) issue_tile<8, 8, 1>(t, nv, lds_to, ln);
-                    else issue_tile<8, 8, 2>(t, nv, lds_to, ln);
-                } else {
-                    if (hf == 0) issue_tile<KB, VB, 1>(t, nv, lds_to, ln);
-                    else issue_tile<KB, VB, 2>(t, nv, lds_to, ln);
-                }
-            } else if (ring) {
+            if (ring) {
                 if constexpr (SMALL) issue_q8_part<0>(t, nv, lds_to, ln);
                 else issue_tile<8, 8>(t, nv, lds_to, ln);
             } else {
@@ -714,17 +696,15 @@ __global__ __launch_bounds__(WIDE ? 512 : 256) __attribute__((amdgpu_waves_per_e
         // the wait (the loaded registers must not be read or moved before it).
         if constexpr (APPEND)
             if (has_new) {
-                const int w0 = WIDE ? hf : 0, w1 = WIDE ? hf : 1; // (the pair's first wave stores K, the second V)
                 append_rows(a.kin, a.vin, a.kin_f16, a.kin_nl, S.ptab, S.pt_stride, S.page, S.n_pages, S.kvrc, SK.vals, SK.scs, SK.ring,
-                            SK.rsc, SK.bits, SK.rot, SV.vals, SV.scs, SV.ring, SV.rsc, SV.bits, SV.rot, seq, g, l, si, L, T, c0, c1, sl, w0, w1);
+                            SK.rsc, SK.bits, SK.rot, SV.vals, SV.scs, SV.ring, SV.rsc, SV.bits, SV.rot, seq, g, l, si, L, T, c0, c1, sl, 0, 1);
                 vm_wait<0>(); // the stored rows are in L2 before this wave's copies read them
             }
-        const int qrow0 = WIDE ? 0 : row0; // the workgroup's first row
-        constexpr int QPW = NQ / NW;       // rows per wave
+        constexpr int QPW = RP / AWAVES; // rows per wave
         f32x4 qx[QPW];
 #pragma unroll
         for (int j = 0; j < QPW; j++) {
-            const int r = qrow0 + wv + NW * j;
+            const int r = row0 + wv + AWAVES * j;
             if (r < a.R) {
                 const int hh = r / T, t = r % T;
                 qx[j] = gload16(a.q + (((size_t) (l * a.nseq + si) * T + t) * NH + GQA * g + hh) * a.qs + 4 * lane);
@@ -733,18 +713,10 @@ __global__ __launch_bounds__(WIDE ? 512 : 256) __attribute__((amdgpu_waves_per_e
             }
         }
         if (my > 0) {
-            issue(0, phys_cur, lds0 + stage_of(0) * SB);
+            issue(0, phys_cur, st_lds);
             // copy instructions of tile 0 (issue_tile / issue_q8_part): every load before them has returned
             const bool ring = S.kvrc > 0 && c0 + ATP * sl >= ws;
-            if constexpr (WIDE) {
-                if (hf == 0) {
-                    if (ring) vm_wait<8 + 1>();
-                    else vm_wait<KB + 1>();
-                } else {
-                    if (ring) vm_wait<8 + 1>();
-                    else vm_wait<VB + 1>();
-                }
-            } else if (ring) {
+            if (ring) {
                 vm_wait<SMALL ? 8 + 1 : 8 + 8 + 1>();
             } else {
                 vm_wait<KB + VB + 1>();
@@ -755,7 +727,7 @@ __global__ __launch_bounds__(WIDE ? 512 : 256) __attribute__((amdgpu_waves_per_e
 #pragma unroll
         for (int j = 0; j < QPW; j++) {
             pin_after(qx[j]);
-            const int r = wv + NW * j, gr = qrow0 + r;
+            const int r = wv + AWAVES * j, gr = row0 + r;
             half2v o0 = {(_Float16) 0.f, (_Float16) 0.f}, o1 = o0;
             if (gr < a.R) {
                 const int t = gr % T;
@@ -767,7 +739,7 @@ __global__ __launch_bounds__(WIDE ? 512 : 256) __attribute__((amdgpu_waves_per_e
                 o1[0] = (_Float16) (v[2] * 0.0625f);
                 o1[1] = (_Float16) (v[3] * 0.0625f);
             }
-            reinterpret_cast<uint2 *>(sQ + (r / RP) * RP * (HD / 8) + qchunk(r % RP, lane >> 1))[lane & 1] = make_uint2(as_u(o0), as_u(o1));
+            reinterpret_cast<uint2 *>(sQ + qchunk(r, lane >> 1))[lane & 1] = make_uint2(as_u(o0), as_u(o1));
         }
         WaveState<NP> st;
 #pragma unroll
@@ -783,7 +755,7 @@ __global__ __launch_bounds__(WIDE ? 512 : 256) __attribute__((amdgpu_waves_per_e
         __syncthreads(); // the query rows are complete
         if constexpr (NP == 1) {
 #pragma unroll
-            for (int ks = 0; ks < 8; ks++) st.qf[ks] = sQh[qchunk(n >> 1, 8 * q + ks)];
+            for (int ks = 0; ks < 8; ks++) st.qf[ks] = sQ[qchunk(n >> 1, 8 * q + ks)];
         }
         const uint8_t * const stp = smem + wv * SB; // (derived from smem: LDS reads)
         // one tile: operands into registers, then the stage is free and the next tile streams in during the math
@@ -829,23 +801,6 @@ __global__ __launch_bounds__(WIDE ? 512 : 256) __attribute__((amdgpu_waves_per_e
             }
             phys_cur = phys_next;
         };
-        // WIDE: one workgroup barrier per step; tile i + 1 streams into the slice's other stage during tile i's math
-        auto wstep = [&](auto fmt, int i) {
-            constexpr int K2 = decltype(fmt)::kb, V2 = decltype(fmt)::vb;
-            set_prio(my - i);
-            const int phys_next = i + 1 < my ? tile_page(i + 1) : 0;
-            vm_wait<0>();    // this wave's half of tile i has landed
-            __syncthreads(); // both halves of every slice's tile i are staged; every wave is done with tile i - 1
-            if (i + 1 < my) issue(i + 1, phys_next, lds0 + stage_of((i + 1) & 1) * SB);
-            if (i < my) {
-                const uint8_t * const sp = smem + stage_of(i & 1) * SB;
-                RawTile<K2, V2> raw;
-                read_k<K2, V2>(raw, sp, n, q);
-                compute_tile<NP, K2, V2, true>(st, sQh, c0 + ATP * (sl + AWAVES * i), raw,
-                                               [&](RawTile<K2, V2> & r, int tn, int tq) { read_v<K2, V2>(r, sp, tn, tq); });
-            }
-            phys_cur = phys_next;
-        };
         // the wave's window (ring) tiles are its last ones: i >= i_ring, p0 >= ws.  Two loops, one tile format each,
         // keep a single tile body live per loop (one body holding both formats costs registers)
         int i_ring = my;
@@ -854,21 +809,16 @@ __global__ __launch_bounds__(WIDE ? 512 : 256) __attribute__((amdgpu_waves_per_e
             i_ring = d <= 0 ? 0 : min(my, (d + AWAVES * ATP - 1) / (AWAVES * ATP));
         }
         int i = 0;
-        if constexpr (WIDE) { // every wave takes part in the my0 barriers
-            for (; i < i_ring; i++) wstep(Fmt<KB, VB>(), i);
-            for (; i < my0; i++) wstep(Fmt<8, 8>(), i);
-        } else {
-            for (; i < i_ring; i++) step(Fmt<KB, VB>(), i);
-            for (; i < my; i++) step(Fmt<8, 8>(), i);
-        }
-        // ---- merge the 4 waves (slices) of each row in order: M = max m_w, O = sum e_w O_w, l = sum e_w l_w.  Per pass
-        // of 16 rows (two groups) every wave writes its scaled O rows to its own LDS buffer (the stages are free), then
-        // each thread adds the 4 buffers of its rows' waves in slice order.
-        constexpr int OLD = HD + 4;                                           // row stride (floats) of a buffer
-        constexpr int MR = NP == 1 ? 8 : 16;                                  // rows per wave buffer
-        float * const s_m = reinterpret_cast<float *>(smem + NW * MR * OLD * 4); // [NW][RP]
-        float * const s_l = s_m + NW * RP;                                    // [NW][RP]
-        static_assert(NW * MR * OLD * 4 + 2 * NW * RP * 4 <= SLDS, "merge buffers inside the stages");
+        for (; i < i_ring; i++) step(Fmt<KB, VB>(), i);
+        for (; i < my; i++) step(Fmt<8, 8>(), i);
+        // ---- merge the 4 waves in order: M = max m_w, O = sum e_w O_w, l = sum e_w l_w.  Per pass of 16 rows (two
+        // groups) every wave writes its scaled O rows to its own LDS buffer (the stages are free), then each thread
+        // adds the 4 buffers in wave order.
+        constexpr int OLD = HD + 4;                                                   // row stride (floats) of a buffer
+        constexpr int MR = NP == 1 ? 8 : 16;                                          // rows per wave buffer
+        float * const s_m = reinterpret_cast<float *>(smem + AWAVES * MR * OLD * 4); // [AWAVES][RP]
+        float * const s_l = s_m + AWAVES * RP;                                        // [AWAVES][RP]
+        static_assert(AWAVES * MR * OLD * 4 + 2 * AWAVES * RP * 4 <= SLDS, "merge buffers inside the stages");
         __syncthreads(); // every wave is done with its stage
         if (q == 0 && !(n & 1)) {
 #pragma unroll
@@ -878,11 +828,7 @@ __global__ __launch_bounds__(WIDE ? 512 : 256) __attribute__((amdgpu_waves_per_e
             }
         }
         __syncthreads();
-        const int R = a.R;
-        // the merging thread's half (WIDE: threads 256 h .. 256 h + 255 add the buffers of waves 4 h .. 4 h + 3)
-        const int th = WIDE ? threadIdx.x / 256 : 0, tl = threadIdx.x - 256 * th, wb = AWAVES * th;
-        const int trow0 = WIDE ? RP * th : row0, RB = min(RP, R - trow0); // its rows
-        const float * const s_mh = s_m + wb * RP, * const s_mw = s_m + hf * AWAVES * RP; // the thread's / the wave's half
+        const int R = a.R, RB = min(RP, R - row0); // rows of this batch
         constexpr int NPASS = (NP + 1) / 2;
 #pragma unroll
         for (int ps = 0; ps < NPASS; ps++) {
@@ -891,7 +837,7 @@ __global__ __launch_bounds__(WIDE ? 512 : 256) __attribute__((amdgpu_waves_per_e
                 const int h = 2 * ps + hh;
                 if (h < NP) {
                     const int row = 8 * h + (n >> 1);
-                    const float M = fmaxf(fmaxf(s_mw[row], s_mw[RP + row]), fmaxf(s_mw[2 * RP + row], s_mw[3 * RP + row]));
+                    const float M = fmaxf(fmaxf(s_m[row], s_m[RP + row]), fmaxf(s_m[2 * RP + row], s_m[3 * RP + row]));
                     const float e = st.m[h] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(st.m[h] - M);
                     float * o = reinterpret_cast<float *>(smem) + (wv * MR + 8 * hh + (n >> 1)) * OLD + 64 * q + (n & 1);
 #pragma unroll
@@ -902,9 +848,9 @@ __global__ __launch_bounds__(WIDE ? 512 : 256) __attribute__((amdgpu_waves_per_e
             }
             __syncthreads();
             const int nrow = min(16, RB - 16 * ps);
-            for (int idx = tl; idx < nrow * (HD / 4); idx += 256) {
+            for (int idx = threadIdx.x; idx < nrow * (HD / 4); idx += 256) {
                 const int r16 = idx / (HD / 4), c4 = idx % (HD / 4);
-                const float * src = reinterpret_cast<const float *>(smem) + (wb * MR + r16) * OLD + 4 * c4;
+                const float * src = reinterpret_cast<const float *>(smem) + r16 * OLD + 4 * c4;
                 float4 y = *reinterpret_cast<const float4 *>(src);
 #pragma unroll
                 for (int w = 1; w < AWAVES; w++) {
@@ -914,9 +860,257 @@ __global__ __launch_bounds__(WIDE ? 512 : 256) __attribute__((amdgpu_waves_per_e
                     y.z += z.z;
                     y.w += z.w;
                 }
-                *reinterpret_cast<float4 *>(a.part + ((size_t) item * R + trow0 + 16 * ps + r16) * HD + 4 * c4) = y;
+                *reinterpret_cast<float4 *>(a.part + ((size_t) item * R + row0 + 16 * ps + r16) * HD + 4 * c4) = y;
             }
             if (ps + 1 < NPASS) __syncthreads();
+        }
+        if (threadIdx.x < RB) {
+            const int row = threadIdx.x;
+            const float M = fmaxf(fmaxf(s_m[row], s_m[RP + row]), fmaxf(s_m[2 * RP + row], s_m[3 * RP + row]));
+            float lsum = 0.f;
+#pragma unroll
+            for (int w = 0; w < AWAVES; w++) {
+                const float ew = s_m[w * RP + row] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(s_m[w * RP + row] - M);
+                lsum += ew * s_l[w * RP + row];
+            }
+            a.ml[(size_t) item * R + row0 + row] = make_float2(M, lsum);
+        }
+        __syncthreads(); // the LDS is reused by the next item
+    }
+}
+
+// ------------------------------------------------------------------------------------------------ verify kernel
+// 25..48 query rows per kv head (T = 5..8) in one pass over each segment, persistent: one workgroup of 8 waves per CU
+// walks the work items blockIdx.x, + gridDim.x, ...  Waves w and w + 4 take tile slice w (tiles w, w + 4, ..) for rows
+// 0..23 and 24..47 and share the slice's two LDS stages; at step i (after a workgroup barrier) tile i + 1 is copied
+// into the other stage -- the K rows and K scales by the first wave of the pair, the V rows and V scales by the
+// second -- while both compute tile i.  After an item's last step the copies of the next item's first tiles go into the
+// free stages during the merge, so an item starts with them on their way.  A row's
+// slices, tile arithmetic and merge order are those of k_attn: bitwise the same partials.
+// APPEND (mk_kv_append_attend): the new rows are stored before an item's first copy, so nothing is started early.
+template <typename P>
+__device__ __forceinline__ P * uniform_ptr(P * p) {
+    const unsigned long long x = (unsigned long long) p;
+    const unsigned lo = __builtin_amdgcn_readfirstlane((unsigned) x), hi = __builtin_amdgcn_readfirstlane((unsigned) (x >> 32));
+    return reinterpret_cast<P *>(((unsigned long long) hi << 32) | lo);
+}
+struct ItemGeo {
+    int si, seq, L, ws, c0, c1, ntiles, g, l, pbase;
+    SideLayout SK, SV;
+    size_t ring0;
+};
+__device__ __forceinline__ ItemGeo item_geo(const AttnArgs & a, int item) {
+    ItemGeo G;
+    int si = 0;
+#pragma unroll
+    for (int i = 1; i < MAX_SEQ; i++)
+        if (i < a.nseq && item >= a.sd[i].item0) si = i;
+    const SeqDesc sd = a.sd[si];
+    const int local = item - sd.item0, seg = local % sd.nseg, lg = local / sd.nseg;
+    G.si = si;
+    G.seq = sd.seq;
+    G.L = sd.L;
+    G.ws = sd.ws;
+    G.g = lg % NKV;
+    G.l = lg / NKV;
+    G.pbase = sd.pbase;
+    G.c0 = seg * sd.cs;
+    G.c1 = min(sd.L, G.c0 + sd.cs);
+    G.ntiles = (G.c1 - G.c0 + ATP - 1) / ATP;
+    G.SK = a.S.side[a.layer0 + G.l][0];
+    G.SV = a.S.side[a.layer0 + G.l][1];
+    G.ring0 = (size_t) (sd.seq * NKV + G.g) * a.S.kvrc;
+    return G;
+}
+
+template <int KB, int VB, bool APPEND = false>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_verify(AttnArgs a) {
+    constexpr int NP = 3, RP = 24, NW = 2 * AWAVES, QPW = 2 * RP / NW, SB = STAGE_BYTES;
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63, n = lane & 15, q = lane >> 4;
+    const int sl = wv & (AWAVES - 1), hf = wv / AWAVES, row0 = RP * hf;
+    const StoreLayout & S = a.S;
+    const unsigned lds0 = (unsigned) (size_t) (__attribute__((address_space(3))) uint8_t *) smem;
+    auto stage = [&](int b) { return 2 * sl + (b & 1); }; // stage b of the wave's slice
+    half8 * const sQ = reinterpret_cast<half8 *>(smem + NW * SB); // [48][256] fp16, chunk-swizzled per half of 24 rows
+    const half8 * const sQh = sQ + hf * RP * (HD / 8);
+    const int T = a.T, R = a.R;
+
+    auto tile_phys = [&](const ItemGeo & G, int p) {
+        return G.pbase >= 0 ? G.pbase + __builtin_amdgcn_readfirstlane(p / S.page) : page_of(S, G.seq, p);
+    };
+    // the wave's half of tile i of an item (its first position c0, length L, window start ws, kv head g, sides SK / SV,
+    // first ring row ring0) into stage b
+    auto issue = [&](SideLayout SK, SideLayout SV, int c0, int L, int ws, int g, size_t ring0, int i, int phys, int b) {
+        const int p0 = c0 + ATP * (sl + AWAVES * i), nv = min(ATP, L - p0);
+        const bool ring = S.kvrc > 0 && p0 >= ws;
+        TileSrc t = tile_src<KB, VB>(S, SK, SV, g, p0, phys, ring0, ring);
+        t.k = uniform_ptr(t.k); // (wave-uniform by construction; stated, so that the copies take the scalar base)
+        t.v = uniform_ptr(t.v);
+        const unsigned to = (unsigned) __builtin_amdgcn_readfirstlane(lds0 + stage(b) * SB);
+        int ln = lane;
+        asm volatile("" : "+v"(ln));
+        if (ring) {
+            if (hf == 0) issue_tile<8, 8, 1>(t, nv, to, ln);
+            else issue_tile<8, 8, 2>(t, nv, to, ln);
+        } else {
+            if (hf == 0) issue_tile<KB, VB, 1>(t, nv, to, ln);
+            else issue_tile<KB, VB, 2>(t, nv, to, ln);
+        }
+    };
+    // the wave's query rows r = wv + 8 j of item G (rows hh T + t of the kv head)
+    auto q_addr = [&](const ItemGeo & G, int j) {
+        const int r = wv + NW * j, hh = r / T, t = r % T;
+        return a.q + (((size_t) (G.l * a.nseq + G.si) * T + t) * NH + GQA * G.g + hh) * a.qs + 4 * lane;
+    };
+
+    int par = 0;      // stage parity of the item's tile 0
+    bool pre = false; // the item's first tiles were started by the previous item
+    for (int item = blockIdx.x; item < a.n_items; item += gridDim.x) {
+        const ItemGeo G = item_geo(a, item);
+        const SideLayout SK = G.SK, SV = G.SV;
+        const int my = G.ntiles > sl ? (G.ntiles - sl + AWAVES - 1) / AWAVES : 0;
+        const int my0 = (G.ntiles + AWAVES - 1) / AWAVES;
+        const int nxt = item + gridDim.x;
+        const bool chain = !(APPEND && a.kin) && nxt < a.n_items;
+        f32x4 qx[QPW];
+        if (pre) { // (tile 0 was copied during the previous merge: waiting for the rows finds it landed too)
+#pragma unroll
+            for (int j = 0; j < QPW; j++)
+                qx[j] = wv + NW * j < R ? *reinterpret_cast<const f32x4 *>(q_addr(G, j)) : f32x4{0.f, 0.f, 0.f, 0.f};
+        } else {
+            if constexpr (APPEND) {
+                bool has_new = false;
+                if (a.kin)
+                    for (int p = max(G.L - T, G.c0); p < min(G.L, G.c1); p++) has_new |= ((p - G.c0) >> 5) % AWAVES == sl;
+                if (has_new) {
+                    append_rows(a.kin, a.vin, a.kin_f16, a.kin_nl, S.ptab, S.pt_stride, S.page, S.n_pages, S.kvrc, G.SK.vals, G.SK.scs,
+                                G.SK.ring, G.SK.rsc, G.SK.bits, G.SK.rot, G.SV.vals, G.SV.scs, G.SV.ring, G.SV.rsc, G.SV.bits, G.SV.rot,
+                                G.seq, G.g, G.l, G.si, G.L, T, G.c0, G.c1, sl, hf, hf);
+                    vm_wait<0>(); // the stored rows are in L2 before this wave's copies read them
+                }
+            }
+            // loaded before the first copy and waited for alone (loads return in order), as in k_attn
+#pragma unroll
+            for (int j = 0; j < QPW; j++) qx[j] = wv + NW * j < R ? gload16(q_addr(G, j)) : f32x4{0.f, 0.f, 0.f, 0.f};
+            if (my > 0) {
+                issue(SK, SV, G.c0, G.L, G.ws, G.g, G.ring0, 0, tile_phys(G, G.c0 + ATP * sl), par);
+                const bool ring = S.kvrc > 0 && G.c0 + ATP * sl >= G.ws;
+                if (ring) vm_wait<8 + 1>();
+                else if (hf == 0) vm_wait<KB + 1>();
+                else vm_wait<VB + 1>();
+            } else {
+                vm_wait<0>();
+            }
+#pragma unroll
+            for (int j = 0; j < QPW; j++) pin_after(qx[j]);
+        }
+        // ---- queries: FWHT when K is stored rotated, * 1/16, fp16 (qwen38_mk.cu:2873-2880)
+#pragma unroll
+        for (int j = 0; j < QPW; j++) {
+            const int r = wv + NW * j;
+            half2v o0 = {(_Float16) 0.f, (_Float16) 0.f}, o1 = o0;
+            if (r < R) {
+                const int t = r % T;
+                float v[4] = {qx[j][0], qx[j][1], qx[j][2], qx[j][3]};
+                if (a.qnw) qk_prep(v, a.qnw + (size_t) G.l * HD, a.rope + (size_t) (G.L - T + t) * 32);
+                if ((a.krot >> (a.layer0 + G.l)) & 1u) fwht256_w64(v);
+                o0[0] = (_Float16) (v[0] * 0.0625f);
+                o0[1] = (_Float16) (v[1] * 0.0625f);
+                o1[0] = (_Float16) (v[2] * 0.0625f);
+                o1[1] = (_Float16) (v[3] * 0.0625f);
+            }
+            reinterpret_cast<uint2 *>(sQ + (r / RP) * RP * (HD / 8) + qchunk(r % RP, lane >> 1))[lane & 1] = make_uint2(as_u(o0), as_u(o1));
+        }
+        WaveState<NP> st;
+#pragma unroll
+        for (int h = 0; h < NP; h++) {
+            st.m[h] = -INFINITY;
+            st.l[h] = 0.f;
+            const int row = row0 + 8 * h + (n >> 1);
+            st.lim[h] = row < R ? G.L - T + row % T : -1;
+#pragma unroll
+            for (int b = 0; b < 8; b++) st.acc[h][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+        st.lim_min = G.L - T;
+        // ---- the tiles: one workgroup barrier per step (the first also completes the query rows)
+        int i_ring = my;
+        if (S.kvrc > 0) {
+            const int d = G.ws - G.c0 - ATP * sl;
+            i_ring = d <= 0 ? 0 : min(my, (d + AWAVES * ATP - 1) / (AWAVES * ATP));
+        }
+        auto vstep = [&](auto fmt, int i) {
+            constexpr int K2 = decltype(fmt)::kb, V2 = decltype(fmt)::vb;
+            set_prio(my - i);
+            const int phys_next = i + 1 < my ? tile_phys(G, G.c0 + ATP * (sl + AWAVES * (i + 1))) : 0;
+            vm_wait<0>();    // this wave's half of tile i has landed
+            __syncthreads(); // both halves of every slice's tile i are staged; every wave is done with tile i - 1
+            if (i + 1 < my) issue(SK, SV, G.c0, G.L, G.ws, G.g, G.ring0, i + 1, phys_next, par + i + 1);
+            if (i < my) {
+                const uint8_t * const sp = smem + stage(par + i) * SB;
+                RawTile<K2, V2> raw;
+                read_k<K2, V2>(raw, sp, n, q);
+                compute_tile<NP, K2, V2, true>(st, sQh, G.c0 + ATP * (sl + AWAVES * i), raw,
+                                               [&](RawTile<K2, V2> & r, int tn, int tq) { read_v<K2, V2>(r, sp, tn, tq); });
+            }
+        };
+        int i = 0;
+        for (; i < i_ring; i++) vstep(Fmt<KB, VB>(), i);
+        for (; i < my0; i++) vstep(Fmt<8, 8>(), i);
+        // the next item's first tile of this slice, on its way during the merge (into the stage parity the last step left
+        // free: its tile my0 - 2 was read before that step's barrier)
+        if (chain) {
+            const ItemGeo N = item_geo(a, nxt);
+            if (N.ntiles > sl) issue(N.SK, N.SV, N.c0, N.L, N.ws, N.g, N.ring0, 0, tile_phys(N, N.c0 + ATP * sl), par + my0);
+        }
+        // ---- merge the 4 slices of each row in order (as k_attn), one 8-row group per pass.  Wave w's buffer is half of
+        // stage 2 (w / 2) + the parity of the last tile (read by now); the next item's first tiles sit in the other parity.
+        constexpr int OLD = HD + 4, MB = 8 * OLD * 4; // row stride (floats), one wave's buffer (bytes)
+        static_assert(2 * MB <= SB, "two wave buffers per stage");
+        const int bl = (par + my0 - 1) & 1;
+        auto wbuf = [&](int w) { return reinterpret_cast<float *>(smem + (2 * (w >> 1) + bl) * SB + (w & 1) * MB); };
+        float * const s_m = reinterpret_cast<float *>(sQ); // [8][24] (the query rows are read by now)
+        float * const s_l = s_m + NW * RP;
+        __syncthreads(); // every wave is done with its tiles and the query rows
+        if (q == 0 && !(n & 1)) {
+#pragma unroll
+            for (int h = 0; h < NP; h++) {
+                s_m[wv * RP + 8 * h + (n >> 1)] = st.m[h];
+                s_l[wv * RP + 8 * h + (n >> 1)] = st.l[h];
+            }
+        }
+        const int th = threadIdx.x / 256, tl = threadIdx.x - 256 * th, wb = AWAVES * th;
+        const int trow0 = RP * th, RB = min(RP, R - trow0);
+        const float * const s_mh = s_m + wb * RP, * const s_mw = s_m + hf * AWAVES * RP;
+        __syncthreads();
+#pragma unroll
+        for (int h = 0; h < NP; h++) {
+            {
+                const int row = 8 * h + (n >> 1);
+                const float M = fmaxf(fmaxf(s_mw[row], s_mw[RP + row]), fmaxf(s_mw[2 * RP + row], s_mw[3 * RP + row]));
+                const float e = st.m[h] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(st.m[h] - M);
+                float * o = wbuf(wv) + (n >> 1) * OLD + 64 * q + (n & 1);
+#pragma unroll
+                for (int b = 0; b < 8; b++)
+#pragma unroll
+                    for (int k = 0; k < 4; k++) o[16 * k + 2 * b] = e * st.acc[h][b][k];
+            }
+            __syncthreads();
+            const int nrow = min(8, RB - 8 * h);
+            for (int idx = tl; idx < nrow * (HD / 4); idx += 256) {
+                const int r8 = idx / (HD / 4), c4 = idx % (HD / 4);
+                float4 y = *reinterpret_cast<const float4 *>(wbuf(wb) + r8 * OLD + 4 * c4);
+#pragma unroll
+                for (int w = 1; w < AWAVES; w++) {
+                    const float4 z = *reinterpret_cast<const float4 *>(wbuf(wb + w) + r8 * OLD + 4 * c4);
+                    y.x += z.x;
+                    y.y += z.y;
+                    y.z += z.z;
+                    y.w += z.w;
+                }
+                *reinterpret_cast<float4 *>(a.part + ((size_t) item * R + trow0 + 8 * h + r8) * HD + 4 * c4) = y;
+            }
+            if (h + 1 < NP) __syncthreads();
         }
         if (tl < RB) {
             const int row = tl;
@@ -929,11 +1123,34 @@ __global__ __launch_bounds__(WIDE ? 512 : 256) __attribute__((amdgpu_waves_per_e
             }
             a.ml[(size_t) item * R + trow0 + row] = make_float2(M, lsum);
         }
-        __syncthreads(); // the LDS is reused by the next item
+        __syncthreads(); // the buffers and the query rows are reused by the next item
+        par = (par + my0) & 1;
+        pre = chain;
     }
 }
 
 typedef void (*AttnKernel)(AttnArgs);
+template <bool APPEND>
+static AttnKernel verify_of(int kb, int vb) {
+#define QKV_VB(K)                                                                                                      \
+    switch (vb) {                                                                                                      \
+    case 4: return k_verify<K, 4, APPEND>;                                                                             \
+    case 5: return k_verify<K, 5, APPEND>;                                                                             \
+    case 6: return k_verify<K, 6, APPEND>;                                                                             \
+    case 7: return k_verify<K, 7, APPEND>;                                                                             \
+    case 8: return k_verify<K, 8, APPEND>;                                                                             \
+    default: return nullptr;                                                                                           \
+    }
+    switch (kb) {
+    case 4: QKV_VB(4)
+    case 5: QKV_VB(5)
+    case 6: QKV_VB(6)
+    case 7: QKV_VB(7)
+    case 8: QKV_VB(8)
+    default: return nullptr;
+    }
+#undef QKV_VB
+}
 // the fused-append kernels (kv_attn_fused.hip): np row groups, wide (np = 3, 48 rows), K / V bits
 AttnKernel pick_fused(int np, bool wide, int kb, int vb);
 

@@ -1,18 +1,19 @@
 // The decode kernels with the fused append (mk_kv_append_attend): k_attn<.., APPEND = true> for every row-group count
-// and K / V format, in a translation unit of their own so that they compile beside the plain kernels.
+// and k_verify<.., APPEND = true>, for every K / V format, in a translation unit of their own so that they compile
+// beside the plain kernels.
 #include "kv_attn_decode.h"
 
 namespace qkv {
 
-template <int NP, bool WIDE>
+template <int NP>
 static AttnKernel fused_of(int kb, int vb) {
 #define QKV_VB(K)                                                                                                      \
     switch (vb) {                                                                                                      \
-    case 4: return k_attn<NP, K, 4, false, WIDE, true>;                                                                \
-    case 5: return k_attn<NP, K, 5, false, WIDE, true>;                                                                \
-    case 6: return k_attn<NP, K, 6, false, WIDE, true>;                                                                \
-    case 7: return k_attn<NP, K, 7, false, WIDE, true>;                                                                \
-    case 8: return k_attn<NP, K, 8, false, WIDE, true>;                                                                \
+    case 4: return k_attn<NP, K, 4, false, true>;                                                                      \
+    case 5: return k_attn<NP, K, 5, false, true>;                                                                      \
+    case 6: return k_attn<NP, K, 6, false, true>;                                                                      \
+    case 7: return k_attn<NP, K, 7, false, true>;                                                                      \
+    case 8: return k_attn<NP, K, 8, false, true>;                                                                      \
     default: return nullptr;                                                                                           \
     }
     switch (kb) {
@@ -27,9 +28,9 @@ static AttnKernel fused_of(int kb, int vb) {
 }
 
 AttnKernel pick_fused(int np, bool wide, int kb, int vb) {
-    if (np == 1) return fused_of<1, false>(kb, vb);
-    if (np == 2) return fused_of<2, false>(kb, vb);
-    if (np == 3) return wide ? fused_of<3, true>(kb, vb) : fused_of<3, false>(kb, vb);
+    if (np == 1) return fused_of<1>(kb, vb);
+    if (np == 2) return fused_of<2>(kb, vb);
+    if (np == 3) return wide ? verify_of<true>(kb, vb) : fused_of<3>(kb, vb);
     return nullptr;
 }
 

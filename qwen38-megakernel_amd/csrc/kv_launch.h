@@ -27,7 +27,7 @@ struct AttnArgs {
     int nseq;
     int n_base;          // (sequence, layer, kv head, segment) work items
     int n_items;         // n_base (wide), else n_base * ceil(R / RP): every item once per row batch (batch-minor)
-    int wide;            // R > 24 in one pass: 8-wave workgroups, waves 4..7 holding rows 24..47
+    int wide;            // R > 24 in one pass (k_verify: persistent 8-wave workgroups, waves 4..7 holding rows 24..47)
     unsigned krot, vrot; // per-slot bit masks: K / V stored rotated
     SeqDesc sd[8];
     const float * q;     // [nl][nseq][T][NH][HD] queries of this launch's layers (fp32, before the 1/16 scale)

@@ -187,6 +187,38 @@ def test_multi_sequence_paged(qkv, oracle, torch_gpu):
         assert np.array_equal(run_attend(torch, flat, Q[:, s:s + 1], [0], [L], 1)[:, 0], out[:, s]), s
 
 
+def test_verify_multi_sequence_paged(qkv, oracle, torch_gpu):
+    """T = 8 over three paged sequences of different lengths (the persistent verify kernel walks work items of several
+    sequences and layers): bitwise equal to the two-batch kernel, also with a grid of 5 workgroups, and sequences 0 and
+    2 within tolerance of the oracle."""
+    torch = torch_gpu
+    rng = np.random.default_rng(18)
+    lens, T = [704, 17000, 20100], 8
+    ctx, page = 20224, 256
+    npg = ctx // page
+    print(f"verify paged lens={lens}", flush=True)
+    st = qkv.KVStore("K*=5r,V*=6", win=2048, n_layers=2, n_seq=3, ctx=ctx, page=page, n_pages=3 * npg)
+    perm = rng.permutation(3 * npg)
+    data = []
+    for s, L in enumerate(lens):
+        st.set_pages(s, perm[s * npg:(s + 1) * npg])
+        K, V = synth_kv(rng, L, 2, outliers=True)
+        append_all(torch, st, s, K, V, chunks=[4096] * 8)
+        data.append((K, V))
+    Q = rng.standard_normal((2, 3, T, NH, HD)).astype(np.float32)
+    out = run_attend(torch, st, Q, [0, 1, 2], lens, T)
+    for s in (0, 2):
+        K, V = data[s]
+        ref = expected_attention(oracle, Q[1, s], K[:, 1], V[:, 1], T, 1, 0, 5, 6, qkv.window_start(lens[s], 2048), True, True)
+        assert rel_err(out[1, s], ref) <= TOL, s
+    st.config("wide", 0)
+    assert np.array_equal(run_attend(torch, st, Q, [0, 1, 2], lens, T), out)
+    st.config("wide", 1)
+    st.config("max_blocks", 5)
+    assert np.array_equal(run_attend(torch, st, Q, [0, 1, 2], lens, T), out)
+    st.config("max_blocks", 0)
+
+
 def test_attend_errors(qkv, torch_gpu):
     st = qkv.KVStore("K*=5r,V*=6", win=1024, n_layers=1, ctx=4000)
     assert qkv.window_start(3201, 1024) != qkv.window_start(3194, 1024)

@@ -44,6 +44,11 @@ def py_dg_hash(b, h=0xcbf29ce484222325):
 
 def test_dg_hash_known_words(oracle):
     assert oracle.dg_hash(np.zeros(0, np.uint8)) == 0xcbf29ce484222325
+    # inputs under 8 bytes take only the byte loop, which is FNV-1a 64: the published FNV-1a test vectors (the FNV
+    # reference test suite of Fowler, Noll and Vo) pin it independently of any restatement
+    for text, want in [(b"a", 0xaf63dc4c8601ec8c), (b"b", 0xaf63df4c8601f1a5), (b"foo", 0xdcb27518fed9d577),
+                       (b"foob", 0xdd120e790c2512af), (b"fooba", 0xcac165afa2fef40a), (b"foobar", 0x85944171f73967e8)]:
+        assert oracle.dg_hash(np.frombuffer(text, np.uint8)) == want, text
     one = ((0xcbf29ce484222325 ^ 0x61) * 0x100000001b3) & MASK64
     assert oracle.dg_hash(np.frombuffer(b"a", np.uint8)) == one
     w = int.from_bytes(b"abcdefgh", "little")

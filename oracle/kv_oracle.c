@@ -23,7 +23,8 @@
  *                      one dominant key -> that V row, L = 1 -> V row) in the tests.
  *   kvo_attn_chunked   the reference's split-K arithmetic (attn_dims chunks, 32-position tiles, fp16 operands,
  *                      fp32 online softmax, attn_combine); pinned against kvo_attn_exact within 2e-3.
- *   kvo_dg_hash        FNV-style row hash; pinned by hand-computed words for short inputs.
+ *   kvo_dg_hash        FNV-style row hash; its byte loop is FNV-1a 64, pinned by the published FNV-1a test vectors;
+ *                      its 8-byte word step by hand-computed words.
  *   kvo_gate           y / (1 + expf(-g)) (qwen38_mk.cu:4686); pinned by closed forms (g = 0 -> y / 2, large g -> y).
  *   kvo_q32_row        q32_store (qwen38_mk.cu:283-307) over one token's 24 x 256 output row: known answers (zero
  *                      block, single value -> +-127, half-away-from-zero ties) and the unit layout by hand-placed

@@ -230,6 +230,8 @@ def test_attend_errors(qkv, torch_gpu):
         st.attend(0, 1, [0], [4001], 1, 1, 1)
     with pytest.raises(qkv.KVError, match="occupancy"):
         st.config("occupancy", 1)
+    with pytest.raises(qkv.KVError, match="wide"):
+        st.config("wide", 2)
     with pytest.raises(qkv.KVError, match="unknown knob"):
         st.config("no_such_knob", 0)
 

@@ -379,8 +379,8 @@ def main():
                     help="only run 5 plain device copies of MIB MiB (the byte-counter calibration for rocprofv3 --pmc)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py: this build measures one GPU only (the KV path shards by kv head / sequence / context with no "
-              "collective in this round); run with --gpus 1", file=sys.stderr)
+        print("bench.py: this build measures one GPU only (the KV path would shard by kv head / sequence / context; "
+              "no multi-GPU path is built); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
     import torch
     torch.cuda.set_device(0)

@@ -566,6 +566,160 @@ __device__ __forceinline__ void compute_tile(WaveState<NP> & st, const half8 * s
     }
 }
 
+// ------------------------------------------------------------------------------------------------ 24-row tile
+// compute_tile for the 24 rows of a k_verify wave with each score computed once: the S^T MFMAs take 16 distinct query
+// rows per column block (block 0: rows 0..15, block 1: rows 16..23 and, in lanes 8..15, copies of them), so the
+// online softmax runs over two blocks instead of three (8 + 8 + 8)-row groups held twice.  The P V operands keep
+// compute_tile's (row, dim parity) column pairs: group h's lane n takes row 8 h + n / 2's fp16 P from the lane that
+// owns that row (ds_bpermute within the lane's 16-lane row).  A row's scores, softmax, P and P V are the same
+// operations on the same values as in compute_tile (an MFMA output element does not depend on its column): bitwise
+// the same partials as k_attn's 24-row kernel.
+struct VerifyState {
+    f32x4 acc[3][8]; // as WaveState<3>::acc: group h, lane (n, q) -> row 8 h + n / 2
+    float m[2], l[2];
+    int lim[2];      // last visible position of the lane's block row 16 H + n (-1: padding)
+    int lim_min;
+};
+
+template <int KB, int VB, typename FV>
+__device__ __forceinline__ void compute_tile_v(VerifyState & st, const half8 * sQ, int p0, RawTile<KB, VB> & raw, FV load_v) {
+    int lane = lane_id();
+    asm volatile("" : "+v"(lane));
+    const int q = lane >> 4, n = lane & 15;
+    f32x4 s[2][2];
+#pragma unroll
+    for (int H = 0; H < 2; H++) s[H][0] = s[H][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < 8; ks++) {
+        const half8 a0 = kfrag<KB>(raw.k0, ks);
+        const half8 a1 = kfrag<KB>(raw.k1, ks);
+#pragma unroll
+        for (int H = 0; H < 2; H++) {
+            const half8 b = sQ[qchunk(H ? 16 + (n & 7) : n, 8 * q + ks)];
+            s[H][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, b, s[H][0], 0, 0, 0);
+            s[H][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, b, s[H][1], 0, 0, 0);
+        }
+    }
+    constexpr float RESCALE_LOG2 = 8.f;
+    const bool full = __builtin_amdgcn_readfirstlane(p0 + ATP - 1 <= st.lim_min);
+    unsigned w[2][2][2]; // block H, group G, pair k: the lane's fp16 P of positions 16 G + 4 q + 2 k, + 1
+    float alpha[2];
+    bool rescale = false;
+#pragma unroll
+    for (int H = 0; H < 2; H++) {
+        float t[8];
+        float mx = -INFINITY;
+        if (full) {
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                t[e] = (e < 4 ? s[H][0][e] : s[H][1][e - 4]) * LOG2E;
+                mx = fmaxf(mx, t[e]);
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const int pos = p0 + (e < 4 ? 4 * q + e : 16 + 4 * q + e - 4);
+                const float sv = (e < 4 ? s[H][0][e] : s[H][1][e - 4]) * LOG2E;
+                t[e] = pos <= st.lim[H] ? sv : -INFINITY;
+                mx = fmaxf(mx, t[e]);
+            }
+        }
+        mx = quad_max(mx);
+        const float mold = st.m[H];
+        const float mnew = mx > mold + RESCALE_LOG2 ? mx : mold;
+        float al = 1.f, ps = 0.f;
+        float p[8];
+        if (mnew != -INFINITY) {
+            al = mold == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mold - mnew);
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                p[e] = __builtin_amdgcn_exp2f(t[e] - mnew);
+                ps += p[e];
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; e++) p[e] = 0.f;
+        }
+        ps = quad_sum(ps);
+        st.l[H] = __builtin_fmaf(st.l[H], al, ps);
+        st.m[H] = mnew;
+        alpha[H] = al;
+        rescale |= al != 1.f && mold != -INFINITY && (H == 0 || n < 8);
+#pragma unroll
+        for (int G = 0; G < 2; G++)
+#pragma unroll
+            for (int k = 0; k < 2; k++) {
+                half2v x2;
+                x2[0] = (_Float16) p[4 * G + 2 * k];
+                x2[1] = (_Float16) p[4 * G + 2 * k + 1];
+                w[H][G][k] = as_u(x2);
+            }
+    }
+    // group h's lane n takes row 8 h + n / 2: block h / 2, lane (8 h + n / 2) % 16 of the same 16-lane row
+    const int src[3] = {4 * (16 * q + (n >> 1)), 4 * (16 * q + 8 + (n >> 1)), 4 * (16 * q + (n >> 1))};
+    if (__any(rescale)) { // alpha == 1 exactly leaves O unchanged: the skip is exact
+#pragma unroll
+        for (int h = 0; h < 3; h++) {
+            const float a = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(src[h], __builtin_bit_cast(int, alpha[h >> 1])));
+#pragma unroll
+            for (int b = 0; b < 8; b++) st.acc[h][b] *= a;
+        }
+    }
+    const unsigned odd = n & 1;
+    const unsigned sel_lo = odd ? 0x05040c0cu : 0x0c0c0504u, sel_hi = odd ? 0x07060c0cu : 0x0c0c0706u;
+    half8 pb[3][2];
+#pragma unroll
+    for (int h = 0; h < 3; h++)
+#pragma unroll
+        for (int G = 0; G < 2; G++)
+#pragma unroll
+            for (int k = 0; k < 2; k++) {
+                const unsigned x = (unsigned) __builtin_amdgcn_ds_bpermute(src[h], (int) w[h >> 1][G][k]);
+                const half2v y0 = as_h2(perm_b32(x, 0u, sel_lo)), y1 = as_h2(perm_b32(x, 0u, sel_hi));
+                pb[h][G][4 * k] = y0[0];
+                pb[h][G][4 * k + 1] = y0[1];
+                pb[h][G][4 * k + 2] = y1[0];
+                pb[h][G][4 * k + 3] = y1[1];
+            }
+    load_v(raw, n, q);
+    lds_drain();
+    // ---- O += P V as compute_tile
+    half2v dv[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) dv[j] = as_h2((raw.v.s[j] & 0xffffu) * 0x10001u);
+    constexpr unsigned QX = VB == 8 ? 0x80808080u : 0u;
+    constexpr float VBIAS = VB == 8 ? 1152.f : (float) (1024 + (1 << (VB - 1)));
+    const half2v vb2 = {(_Float16) -VBIAS, (_Float16) -VBIAS};
+#pragma unroll
+    for (int wd = 0; wd < 2; wd++) {
+        unsigned c[8][2];
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            vcodes_word<VB>(raw.v, j, wd, c[j]);
+            c[j][0] ^= QX;
+            c[j][1] ^= QX;
+        }
+#pragma unroll
+        for (int bb = 0; bb < 4; bb++) {
+            const int b = 4 * wd + bb;
+            const unsigned sel = (bb & 1) ? 0x00070006u : 0x00050004u;
+#pragma unroll
+            for (int G = 0; G < 2; G++) {
+                half8 va;
+#pragma unroll
+                for (int jj = 0; jj < 4; jj++) {
+                    const int j = 4 * G + jj;
+                    const half2v x = (as_h2(perm_b32(c[j][bb >> 1], C64, sel)) + vb2) * dv[j];
+                    va[2 * jj] = x[0];
+                    va[2 * jj + 1] = x[1];
+                }
+#pragma unroll
+                for (int h = 0; h < 3; h++) st.acc[h][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb[h][G], st.acc[h][b], 0, 0, 0);
+            }
+        }
+    }
+}
+
 // The fused append's rows of one wave (mk_kv_append_attend): positions L - T .. L - 1 of segment [c0, c1) whose tile
 // falls in slice sl, sides w0 .. w1 (0 = K, 1 = V), each stored by store_row exactly as k_append stores it.  Plain
 // values (a called function: inlined, its code made the fused kernels' tile loop slower); called only from the
@@ -1022,16 +1176,18 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             }
             reinterpret_cast<uint2 *>(sQ + (r / RP) * RP * (HD / 8) + qchunk(r % RP, lane >> 1))[lane & 1] = make_uint2(as_u(o0), as_u(o1));
         }
-        WaveState<NP> st;
+        VerifyState st;
 #pragma unroll
-        for (int h = 0; h < NP; h++) {
-            st.m[h] = -INFINITY;
-            st.l[h] = 0.f;
-            const int row = row0 + 8 * h + (n >> 1);
-            st.lim[h] = row < R ? G.L - T + row % T : -1;
+        for (int H = 0; H < 2; H++) {
+            st.m[H] = -INFINITY;
+            st.l[H] = 0.f;
+            const int row = row0 + 16 * H + n; // (block 1, lanes 8..15: padding)
+            st.lim[H] = (H == 0 || n < 8) && row < R ? G.L - T + row % T : -1;
+        }
+#pragma unroll
+        for (int h = 0; h < NP; h++)
 #pragma unroll
             for (int b = 0; b < 8; b++) st.acc[h][b] = f32x4{0.f, 0.f, 0.f, 0.f};
-        }
         st.lim_min = G.L - T;
         // ---- the tiles: one workgroup barrier per step (the first also completes the query rows)
         int i_ring = my;
@@ -1050,7 +1206,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                 const uint8_t * const sp = smem + stage(par + i) * SB;
                 RawTile<K2, V2> raw;
                 read_k<K2, V2>(raw, sp, n, q);
-                compute_tile<NP, K2, V2, true>(st, sQh, G.c0 + ATP * (sl + AWAVES * i), raw,
+                compute_tile_v<K2, V2>(st, sQh, G.c0 + ATP * (sl + AWAVES * i), raw,
                                                [&](RawTile<K2, V2> & r, int tn, int tq) { read_v<K2, V2>(r, sp, tn, tq); });
             }
         };
@@ -1072,11 +1228,12 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         float * const s_m = reinterpret_cast<float *>(sQ); // [8][24] (the query rows are read by now)
         float * const s_l = s_m + NW * RP;
         __syncthreads(); // every wave is done with its tiles and the query rows
-        if (q == 0 && !(n & 1)) {
-#pragma unroll
-            for (int h = 0; h < NP; h++) {
-                s_m[wv * RP + 8 * h + (n >> 1)] = st.m[h];
-                s_l[wv * RP + 8 * h + (n >> 1)] = st.l[h];
+        if (q == 0) { // rows 16 H + n of the blocks
+            s_m[wv * RP + n] = st.m[0];
+            s_l[wv * RP + n] = st.l[0];
+            if (n < 8) {
+                s_m[wv * RP + 16 + n] = st.m[1];
+                s_l[wv * RP + 16 + n] = st.l[1];
             }
         }
         const int th = threadIdx.x / 256, tl = threadIdx.x - 256 * th, wb = AWAVES * th;
@@ -1088,7 +1245,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             {
                 const int row = 8 * h + (n >> 1);
                 const float M = fmaxf(fmaxf(s_mw[row], s_mw[RP + row]), fmaxf(s_mw[2 * RP + row], s_mw[3 * RP + row]));
-                const float e = st.m[h] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(st.m[h] - M);
+                const float mr = s_mw[wv % AWAVES * RP + row]; // the wave's own m of the row
+                const float e = mr == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mr - M);
                 float * o = wbuf(wv) + (n >> 1) * OLD + 64 * q + (n & 1);
 #pragma unroll
                 for (int b = 0; b < 8; b++)

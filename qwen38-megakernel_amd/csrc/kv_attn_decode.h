@@ -24,6 +24,7 @@
 // This header holds the decode kernel template (k_attn) and its device helpers: kv_attn.hip instantiates the plain
 // kernels, kv_attn_fused.hip the ones with the fused append (mk_kv_append_attend), in two translation units.
 #pragma once
+#include <type_traits>
 #include "kv_dev.h"
 #include "kv_launch.h"
 
@@ -567,34 +568,40 @@ __device__ __forceinline__ void compute_tile(WaveState<NP> & st, const half8 * s
 }
 
 // ------------------------------------------------------------------------------------------------ 24-row tile
-// compute_tile for the 24 rows of a k_verify wave with each score computed once: the S^T MFMAs take 16 distinct query
-// rows per column block (block 0: rows 0..15, block 1: rows 16..23 and, in lanes 8..15, copies of them), so the
-// online softmax runs over two blocks instead of three (8 + 8 + 8)-row groups held twice.  The P V operands keep
+// compute_tile for 16 or 24 rows (NP = 2, 3) with each score computed once: the S^T MFMAs take 16 distinct query rows
+// per column block (block 0: rows 0..15, block 1: rows 16..23 and, in lanes 8..15, copies of them), so the online
+// softmax runs over NB = 1 or 2 blocks instead of NP 8-row groups held twice.  The P V operands keep
 // compute_tile's (row, dim parity) column pairs: group h's lane n takes row 8 h + n / 2's fp16 P from the lane that
 // owns that row (ds_bpermute within the lane's 16-lane row).  A row's scores, softmax, P and P V are the same
 // operations on the same values as in compute_tile (an MFMA output element does not depend on its column): bitwise
 // the same partials as k_attn's 24-row kernel.
-struct VerifyState {
-    f32x4 acc[3][8]; // as WaveState<3>::acc: group h, lane (n, q) -> row 8 h + n / 2
-    float m[2], l[2];
-    int lim[2];      // last visible position of the lane's block row 16 H + n (-1: padding)
+template <int NP>
+struct RowState {
+    static constexpr int NB = (NP + 1) / 2;
+    f32x4 acc[NP][8]; // as WaveState::acc: group h, lane (n, q) -> row 8 h + n / 2
+    float m[NB], l[NB];
+    int lim[NB];      // last visible position of the lane's block row 16 H + n (-1: padding)
     int lim_min;
 };
 
-template <int KB, int VB, typename FV>
-__device__ __forceinline__ void compute_tile_v(VerifyState & st, const half8 * sQ, int p0, RawTile<KB, VB> & raw, FV load_v) {
+// load_v(raw, n, q) reads the V operands after the scores; after_v() runs once they are in registers
+template <int NP, int KB, int VB, typename FV, typename FA = NoHook>
+__device__ __forceinline__ void compute_tile_v(RowState<NP> & st, const half8 * sQ, int p0, RawTile<KB, VB> & raw, FV load_v,
+                                               FA after_v = FA()) {
+    static_assert(NP == 2 || NP == 3, "16 or 24 rows");
+    constexpr int NB = RowState<NP>::NB;
     int lane = lane_id();
     asm volatile("" : "+v"(lane));
     const int q = lane >> 4, n = lane & 15;
-    f32x4 s[2][2];
+    f32x4 s[NB][2];
 #pragma unroll
-    for (int H = 0; H < 2; H++) s[H][0] = s[H][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int H = 0; H < NB; H++) s[H][0] = s[H][1] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int ks = 0; ks < 8; ks++) {
         const half8 a0 = kfrag<KB>(raw.k0, ks);
         const half8 a1 = kfrag<KB>(raw.k1, ks);
 #pragma unroll
-        for (int H = 0; H < 2; H++) {
+        for (int H = 0; H < NB; H++) {
             const half8 b = sQ[qchunk(H ? 16 + (n & 7) : n, 8 * q + ks)];
             s[H][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, b, s[H][0], 0, 0, 0);
             s[H][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, b, s[H][1], 0, 0, 0);
@@ -602,11 +609,11 @@ __device__ __forceinline__ void compute_tile_v(VerifyState & st, const half8 * s
     }
     constexpr float RESCALE_LOG2 = 8.f;
     const bool full = __builtin_amdgcn_readfirstlane(p0 + ATP - 1 <= st.lim_min);
-    unsigned w[2][2][2]; // block H, group G, pair k: the lane's fp16 P of positions 16 G + 4 q + 2 k, + 1
-    float alpha[2];
+    unsigned w[NB][2][2]; // block H, group G, pair k: the lane's fp16 P of positions 16 G + 4 q + 2 k, + 1
+    float alpha[NB];
     bool rescale = false;
 #pragma unroll
-    for (int H = 0; H < 2; H++) {
+    for (int H = 0; H < NB; H++) {
         float t[8];
         float mx = -INFINITY;
         if (full) {
@@ -659,7 +666,7 @@ __device__ __forceinline__ void compute_tile_v(VerifyState & st, const half8 * s
     const int src[3] = {4 * (16 * q + (n >> 1)), 4 * (16 * q + 8 + (n >> 1)), 4 * (16 * q + (n >> 1))};
     if (__any(rescale)) { // alpha == 1 exactly leaves O unchanged: the skip is exact
 #pragma unroll
-        for (int h = 0; h < 3; h++) {
+        for (int h = 0; h < NP; h++) {
             const float a = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(src[h], __builtin_bit_cast(int, alpha[h >> 1])));
 #pragma unroll
             for (int b = 0; b < 8; b++) st.acc[h][b] *= a;
@@ -667,9 +674,9 @@ __device__ __forceinline__ void compute_tile_v(VerifyState & st, const half8 * s
     }
     const unsigned odd = n & 1;
     const unsigned sel_lo = odd ? 0x05040c0cu : 0x0c0c0504u, sel_hi = odd ? 0x07060c0cu : 0x0c0c0706u;
-    half8 pb[3][2];
+    half8 pb[NP][2];
 #pragma unroll
-    for (int h = 0; h < 3; h++)
+    for (int h = 0; h < NP; h++)
 #pragma unroll
         for (int G = 0; G < 2; G++)
 #pragma unroll
@@ -683,6 +690,7 @@ __device__ __forceinline__ void compute_tile_v(VerifyState & st, const half8 * s
             }
     load_v(raw, n, q);
     lds_drain();
+    after_v();
     // ---- O += P V as compute_tile
     half2v dv[8];
 #pragma unroll
@@ -714,7 +722,7 @@ __device__ __forceinline__ void compute_tile_v(VerifyState & st, const half8 * s
                     va[2 * jj + 1] = x[1];
                 }
 #pragma unroll
-                for (int h = 0; h < 3; h++) st.acc[h][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb[h][G], st.acc[h][b], 0, 0, 0);
+                for (int h = 0; h < NP; h++) st.acc[h][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb[h][G], st.acc[h][b], 0, 0, 0);
             }
         }
     }
@@ -895,16 +903,30 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SMALL ? 3 :
             }
             reinterpret_cast<uint2 *>(sQ + qchunk(r, lane >> 1))[lane & 1] = make_uint2(as_u(o0), as_u(o1));
         }
-        WaveState<NP> st;
+        // one 8-row group: compute_tile (each row in two columns); 16 or 24 rows: compute_tile_v (distinct rows)
+        constexpr bool DISTINCT = NP >= 2;
+        std::conditional_t<DISTINCT, RowState<(DISTINCT ? NP : 2)>, WaveState<NP>> st;
+        if constexpr (DISTINCT) {
 #pragma unroll
-        for (int h = 0; h < NP; h++) {
-            st.m[h] = -INFINITY;
-            st.l[h] = 0.f;
-            const int row = row0 + 8 * h + (n >> 1);
-            st.lim[h] = row < a.R ? L - T + row % T : -1;
+            for (int H = 0; H < RowState<NP>::NB; H++) {
+                st.m[H] = -INFINITY;
+                st.l[H] = 0.f;
+                const int row = row0 + 16 * H + n; // (block 1, lanes 8..15: padding)
+                st.lim[H] = (H == 0 || n < 8) && row < a.R ? L - T + row % T : -1;
+            }
+        } else {
+#pragma unroll
+            for (int h = 0; h < NP; h++) {
+                st.m[h] = -INFINITY;
+                st.l[h] = 0.f;
+                const int row = row0 + 8 * h + (n >> 1);
+                st.lim[h] = row < a.R ? L - T + row % T : -1;
+            }
+        }
+#pragma unroll
+        for (int h = 0; h < NP; h++)
 #pragma unroll
             for (int b = 0; b < 8; b++) st.acc[h][b] = f32x4{0.f, 0.f, 0.f, 0.f};
-        }
         st.lim_min = L - T;
         __syncthreads(); // the query rows are complete
         if constexpr (NP == 1) {
@@ -939,6 +961,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SMALL ? 3 :
                     [&]() {
                         if (i + 1 < my) issue(i + 1, phys_next, st_lds);
                     });
+            } else if constexpr (LATE_V && DISTINCT) {
+                read_k<K2, V2>(raw, stp, n, q);
+                compute_tile_v<(DISTINCT ? NP : 2), K2, V2>(
+                    st, sQ, p0, raw, [&](RawTile<K2, V2> & r, int tn, int tq) { read_v<K2, V2>(r, stp, tn, tq); },
+                    [&]() {
+                        if (i + 1 < my) issue(i + 1, phys_next, st_lds);
+                    });
             } else if constexpr (LATE_V) {
                 read_k<K2, V2>(raw, stp, n, q);
                 compute_tile<NP, K2, V2, true>(
@@ -946,6 +975,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SMALL ? 3 :
                     [&]() {
                         if (i + 1 < my) issue(i + 1, phys_next, st_lds);
                     });
+            } else if constexpr (DISTINCT) {
+                read_k<K2, V2>(raw, stp, n, q);
+                read_v<K2, V2>(raw, stp, n, q);
+                lds_drain();
+                if (i + 1 < my) issue(i + 1, phys_next, st_lds);
+                compute_tile_v<(DISTINCT ? NP : 2), K2, V2>(st, sQ, p0, raw, NoHook());
             } else {
                 read_k<K2, V2>(raw, stp, n, q);
                 read_v<K2, V2>(raw, stp, n, q);
@@ -974,7 +1009,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SMALL ? 3 :
         float * const s_l = s_m + AWAVES * RP;                                        // [AWAVES][RP]
         static_assert(AWAVES * MR * OLD * 4 + 2 * AWAVES * RP * 4 <= SLDS, "merge buffers inside the stages");
         __syncthreads(); // every wave is done with its stage
-        if (q == 0 && !(n & 1)) {
+        if constexpr (DISTINCT) {
+            if (q == 0) { // rows 16 H + n of the blocks
+                s_m[wv * RP + n] = st.m[0];
+                s_l[wv * RP + n] = st.l[0];
+                if constexpr (NP == 3)
+                    if (n < 8) {
+                        s_m[wv * RP + 16 + n] = st.m[RowState<NP>::NB - 1];
+                        s_l[wv * RP + 16 + n] = st.l[RowState<NP>::NB - 1];
+                    }
+            }
+        } else if (q == 0 && !(n & 1)) {
 #pragma unroll
             for (int h = 0; h < NP; h++) {
                 s_m[wv * RP + 8 * h + (n >> 1)] = st.m[h];
@@ -992,7 +1037,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SMALL ? 3 :
                 if (h < NP) {
                     const int row = 8 * h + (n >> 1);
                     const float M = fmaxf(fmaxf(s_m[row], s_m[RP + row]), fmaxf(s_m[2 * RP + row], s_m[3 * RP + row]));
-                    const float e = st.m[h] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(st.m[h] - M);
+                    const float mr = DISTINCT ? s_m[wv * RP + row] : st.m[(DISTINCT ? 0 : h)]; // the wave's own m of the row
+                    const float e = mr == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mr - M);
                     float * o = reinterpret_cast<float *>(smem) + (wv * MR + 8 * hh + (n >> 1)) * OLD + 64 * q + (n & 1);
 #pragma unroll
                     for (int b = 0; b < 8; b++)
@@ -1176,7 +1222,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             }
             reinterpret_cast<uint2 *>(sQ + (r / RP) * RP * (HD / 8) + qchunk(r % RP, lane >> 1))[lane & 1] = make_uint2(as_u(o0), as_u(o1));
         }
-        VerifyState st;
+        RowState<NP> st;
 #pragma unroll
         for (int H = 0; H < 2; H++) {
             st.m[H] = -INFINITY;
@@ -1206,7 +1252,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                 const uint8_t * const sp = smem + stage(par + i) * SB;
                 RawTile<K2, V2> raw;
                 read_k<K2, V2>(raw, sp, n, q);
-                compute_tile_v<K2, V2>(st, sQh, G.c0 + ATP * (sl + AWAVES * i), raw,
+                compute_tile_v<NP, K2, V2>(st, sQh, G.c0 + ATP * (sl + AWAVES * i), raw,
                                                [&](RawTile<K2, V2> & r, int tn, int tq) { read_v<K2, V2>(r, sp, tn, tq); });
             }
         };

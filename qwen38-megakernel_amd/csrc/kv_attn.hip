@@ -405,14 +405,24 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         if (is_ring(i)) pq_dequant<8, 8>(reg, pw, lane, sK, sVt);
         else pq_dequant<KB, VB>(reg, pw, lane, sK, sVt);
     };
-    // ---- query rows: all 8 waves stage 16 rows each (prep, FWHT for rotated K, * 1/16, fp16), consumers take fragments
+    // ---- query rows: all 8 waves stage 16 rows each (prep, FWHT for rotated K, * 1/16, fp16), consumers take fragments;
+    // loaded 8 rows at a time (independent loads, one wait)
     _Float16 * const qs = reinterpret_cast<_Float16 *>(smem);
-    for (int j = 0; j < 16; j++) {
-        const int rl = 16 * wv + j, r = r0 + rl;
+    for (int jb = 0; jb < 16; jb += 8) {
+        float4 xs[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int r = r0 + 16 * wv + jb + u, t = r / GQA, hh = r - GQA * t;
+            xs[u] = r < a.R ? *reinterpret_cast<const float4 *>(a.q + ((size_t) t * NH + GQA * g + hh) * a.qs + 4 * lane)
+                            : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+        const int rl = 16 * wv + jb + u, r = r0 + rl;
         half2v o0 = {(_Float16) 0.f, (_Float16) 0.f}, o1 = o0;
         if (r < a.R) {
-            const int t = r / GQA, hh = r - GQA * t;
-            const float4 x = *reinterpret_cast<const float4 *>(a.q + ((size_t) t * NH + GQA * g + hh) * a.qs + 4 * lane);
+            const int t = r / GQA;
+            const float4 x = xs[u];
             float v[4] = {x.x, x.y, x.z, x.w};
             if (a.qnw) qk_prep(v, a.qnw, a.rope + (size_t) (a.n0 + t) * 32);
             if (a.krot) fwht256_w64(v);
@@ -422,6 +432,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             o1[1] = (_Float16) (v[3] * 0.0625f);
         }
         *reinterpret_cast<uint2 *>(qs + rl * SK_LD + 4 * lane) = make_uint2(as_u(o0), as_u(o1));
+    }
     }
     __syncthreads();
     // Both roles pass the same barriers: two after the staging, then one per tile.

@@ -393,8 +393,9 @@ __device__ __forceinline__ void read_v(RawTile<KB, VB> & r, const uint8_t * st, 
 }
 
 // ------------------------------------------------------------------------------------------------ the tile
-// Query rows go in NP groups of 8 (NP = 1, 2 or 3: 8, 16 or 24 rows per pass).  Both MFMA products use the 16
-// columns as (row, e) pairs, row = 8 h + n / 2 of group h and e = n % 2:
+// Query rows go in NP groups of 8 (compute_tile: one group; 16 and 24 rows take compute_tile_v below, which shares
+// the O += P V form).  Both MFMA products use the 16 columns as (row, e) pairs, row = 8 h + n / 2 of group h and
+// e = n % 2:
 //   S^T = K Q^T   column n of Q^T is query row 8 h + n / 2 (each score is computed in lanes n and n ^ 1), so lane
 //                 (n, q) owns its row's scores at positions 4 q + e and 16 + 4 q + e (e = 0..3);
 //   O += P V      the MFMA's K = 32 is 16 positions x (e = 0, 1):

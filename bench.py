@@ -163,6 +163,19 @@ def bench_cfg3(torch, qkv, steps, warmup):
         pp = profiled(torch, st, lambda: slot_proj(pf), steps)
         proj["prefetch" if pf else "plain"] = {"step_s": t, "attn_kernel_avg_s": pp["attn_ms"] / pp["calls"] * 1e-3}
     del wts
+    # speculative verify over the same store: T query tokens per call (T = 2, 4, 8 -> 12, 24, 48 query rows per kv head),
+    # one-layer calls, us per layer
+    spec = {}
+    for T in (2, 4, 8):
+        qs = torch.randn(nl, 1, T, NH, HD, device="cuda", generator=g)
+        os_ = torch.empty_like(qs)
+        lt = qs[0].numel() * 4
+
+        def spec_step():
+            for l in range(nl):
+                st.attend(l, 1, [0], [L], T, qs.data_ptr() + l * lt, os_.data_ptr() + l * lt)
+
+        spec[f"T{T}_us_per_layer"] = timed(torch, spec_step, steps, warmup) / nl * 1e6
     ok = bool(torch.isfinite(out).all().item())
     return {
         "L": L, "ws": ws, "ring_positions": L - ws, "layers": nl,
@@ -174,7 +187,7 @@ def bench_cfg3(torch, qkv, steps, warmup):
         "fused16_gbps": nl * per_layer_bytes / t_fused / 1e9, "fused16_attn_kernel_avg_s": fused_attn_avg,
         "fused16_attn_kernel_gbps": nl * per_layer_bytes / fused_attn_avg / 1e9,
         "slot_append_then_attend_step_s": t_slot_sep, "slot_append_attend_fused_step_s": t_slot_fused,
-        "slot_after_projection": proj, "finite": ok,
+        "slot_after_projection": proj, "spec_verify": spec, "finite": ok,
     }
 
 

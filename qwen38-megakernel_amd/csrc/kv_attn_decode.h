@@ -248,6 +248,9 @@ __device__ __forceinline__ void dma16s(const void * base, unsigned voff, unsigne
     asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds), "v"(voff), "s"(base) : "memory");
 }
 __device__ __forceinline__ void lds_drain() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+// a workgroup barrier for LDS data only: __syncthreads() also waits for every vector-memory operation of the wave,
+// which would expose the latency of the tile copies in flight at the barrier
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 template <int N>
 __device__ __forceinline__ void vm_wait() {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
@@ -782,7 +785,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SMALL ? 3 :
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     // the wave index as a scalar: tile positions, page lookups and source selection stay scalar (SMEM loads, uniform
     // branches); vector loads there would need vmcnt waits that also drain the tile copies in flight
-    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63, n = lane & 15, q = lane >> 4;
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    // the lane index is made opaque at each item's start and again before its merge: lane-derived values of the start
+    // and the merge are not held (and spilled) across the tile loop, as a spill reload waits for every copy in flight
+    int lane = threadIdx.x & 63;
     const int sl = wv; // the wave's slice of tiles: w, w + 4, ..
     const StoreLayout & S = a.S;
     const unsigned lds0 = (unsigned) (size_t) (__attribute__((address_space(3))) uint8_t *) smem;
@@ -800,6 +806,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SMALL ? 3 :
                  "s"(V0.scs), "s"(V0.ring), "s"(V0.rsc), "s"(a.T), "s"(a.R), "s"(a.layer0), "s"(a.krot), "s"(a.qs), "s"(a.q),
                  "s"(a.qnw), "s"(a.rope), "s"(S.ptab), "s"(S.pt_stride));
     for (int bitem = blockIdx.x; bitem < n_items; bitem += gridDim.x) {
+        asm volatile("" : "+v"(lane));
+        int n = lane & 15, q = lane >> 4;
         const int nb = n_items / n_base, item = bitem / nb, batch = bitem - item * nb, row0 = RP * batch;
         int si = 0;
         SeqDesc sd = sd0;
@@ -1002,6 +1010,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SMALL ? 3 :
         int i = 0;
         for (; i < i_ring; i++) step(Fmt<KB, VB>(), i);
         for (; i < my; i++) step(Fmt<8, 8>(), i);
+        asm volatile("" : "+v"(lane));
+        n = lane & 15;
+        q = lane >> 4;
         // ---- merge the 4 waves in order: M = max m_w, O = sum e_w O_w, l = sum e_w l_w.  Per pass of 16 rows (two
         // groups) every wave writes its scaled O rows to its own LDS buffer (the stages are free), then each thread
         // adds the 4 buffers in wave order.
@@ -1129,7 +1140,11 @@ template <int KB, int VB, bool APPEND = false>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_verify(AttnArgs a) {
     constexpr int NP = 3, RP = 24, NW = 2 * AWAVES, QPW = 2 * RP / NW, SB = STAGE_BYTES;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63, n = lane & 15, q = lane >> 4;
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    // the lane index is made opaque at each item's start and again before its merge, so that lane-derived values of the
+    // item's start and merge are not held (and spilled) across the tile loop: a spill reload waits for every copy in
+    // flight, the next item's first tiles included
+    int lane = threadIdx.x & 63;
     const int sl = wv & (AWAVES - 1), hf = wv / AWAVES, row0 = RP * hf;
     const StoreLayout & S = a.S;
     const unsigned lds0 = (unsigned) (size_t) (__attribute__((address_space(3))) uint8_t *) smem;
@@ -1169,6 +1184,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     int par = 0;      // stage parity of the item's tile 0
     bool pre = false; // the item's first tiles were started by the previous item
     for (int item = blockIdx.x; item < a.n_items; item += gridDim.x) {
+        asm volatile("" : "+v"(lane));
+        int n = lane & 15, q = lane >> 4;
         const ItemGeo G = item_geo(a, item);
         const SideLayout SK = G.SK, SV = G.SV;
         const int my = G.ntiles > sl ? (G.ntiles - sl + AWAVES - 1) / AWAVES : 0;
@@ -1267,6 +1284,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             const ItemGeo N = item_geo(a, nxt);
             if (N.ntiles > sl) issue(N.SK, N.SV, N.c0, N.L, N.ws, N.g, N.ring0, 0, tile_phys(N, N.c0 + ATP * sl), par + my0);
         }
+        asm volatile("" : "+v"(lane));
+        n = lane & 15;
+        q = lane >> 4;
         // ---- merge the 4 slices of each row in order (as k_attn), one 8-row group per pass.  Wave w's buffer is half of
         // stage 2 (w / 2) + the parity of the last tile (read by now); the next item's first tiles sit in the other parity.
         constexpr int OLD = HD + 4, MB = 8 * OLD * 4; // row stride (floats), one wave's buffer (bytes)
@@ -1275,7 +1295,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         auto wbuf = [&](int w) { return reinterpret_cast<float *>(smem + (2 * (w >> 1) + bl) * SB + (w & 1) * MB); };
         float * const s_m = reinterpret_cast<float *>(sQ); // [8][24] (the query rows are read by now)
         float * const s_l = s_m + NW * RP;
-        __syncthreads(); // every wave is done with its tiles and the query rows
+        lds_barrier(); // every wave is done with its tiles and the query rows
         if (q == 0) { // rows 16 H + n of the blocks
             s_m[wv * RP + n] = st.m[0];
             s_l[wv * RP + n] = st.l[0];
@@ -1287,7 +1307,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         const int th = threadIdx.x / 256, tl = threadIdx.x - 256 * th, wb = AWAVES * th;
         const int trow0 = RP * th, RB = min(RP, R - trow0);
         const float * const s_mh = s_m + wb * RP, * const s_mw = s_m + hf * AWAVES * RP;
-        __syncthreads();
+        lds_barrier();
 #pragma unroll
         for (int h = 0; h < NP; h++) {
             {
@@ -1301,7 +1321,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
                     for (int k = 0; k < 4; k++) o[16 * k + 2 * b] = e * st.acc[h][b][k];
             }
-            __syncthreads();
+            lds_barrier();
             const int nrow = min(8, RB - 8 * h);
             for (int idx = tl; idx < nrow * (HD / 4); idx += 256) {
                 const int r8 = idx / (HD / 4), c4 = idx % (HD / 4);
@@ -1316,7 +1336,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                 }
                 *reinterpret_cast<float4 *>(a.part + ((size_t) item * R + trow0 + 8 * h + r8) * HD + 4 * c4) = y;
             }
-            if (h + 1 < NP) __syncthreads();
+            if (h + 1 < NP) lds_barrier();
         }
         if (tl < RB) {
             const int row = tl;
@@ -1329,7 +1349,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             }
             a.ml[(size_t) item * R + trow0 + row] = make_float2(M, lsum);
         }
-        __syncthreads(); // the buffers and the query rows are reused by the next item
+        lds_barrier(); // the buffers and the query rows are reused by the next item
         par = (par + my0) & 1;
         pre = chain;
     }

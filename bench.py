@@ -119,6 +119,17 @@ def bench_cfg3(torch, qkv, steps, warmup):
     prof = profiled(torch, st, step_layers, steps)
     calls = prof["calls"]
     attn_avg = prof["attn_ms"] / calls * 1e-3
+    # the same 16 one-layer calls captured once as a HIP graph and replayed (how a serving loop issues a decode step's
+    # launches; every kernel runs, the graph removes the host's launch cost and the gaps between launches)
+    side = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        step_layers()  # warm (workspace sized, kernel attributes set)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph, stream=side):
+            for l in range(nl):
+                st.attend(l, 1, [0], [L], 1, qp + l * lay, op + l * lay, stream=side.cuda_stream)
+    t_graph = timed(torch, graph.replay, steps, warmup)
     t_fused = timed(torch, step_fused, steps, warmup)
     prof_f = profiled(torch, st, step_fused, steps)
     fused_attn_avg = prof_f["attn_ms"] / prof_f["calls"] * 1e-3
@@ -183,6 +194,7 @@ def bench_cfg3(torch, qkv, steps, warmup):
         "attn_kernel_avg_s": attn_avg, "attn_kernel_bytes": per_layer_bytes,
         "attn_kernel_gbps": per_layer_bytes / attn_avg / 1e9,
         "combine_avg_s": prof["combine_ms"] / calls * 1e-3, "profiled_step_s": prof["step_s"],
+        "graph_step_s": t_graph, "graph_positions_per_s": nl * L / t_graph, "graph_gbps": nl * per_layer_bytes / t_graph / 1e9,
         "fused16_step_s": t_fused, "fused16_positions_per_s": nl * L / t_fused,
         "fused16_gbps": nl * per_layer_bytes / t_fused / 1e9, "fused16_attn_kernel_avg_s": fused_attn_avg,
         "fused16_attn_kernel_gbps": nl * per_layer_bytes / fused_attn_avg / 1e9,

@@ -95,13 +95,14 @@ __device__ __forceinline__ void fwht256_w64(float (&v)[4]) {
                 v[k | m] = a - b;
             }
     const int lane = lane_id();
+    // lane-bit stages: v' = o + s v with s = -1 in the upper lane of each pair (o - v) and +1 in the lower (v + o), one
+    // FMA each: a product with +-1 is exact, so the FMA rounds o +- v once, the same bits as the add or subtract
 #pragma unroll
-    for (int m = 1; m < 64; m <<= 1)
+    for (int m = 1; m < 64; m <<= 1) {
+        const float sg = (lane & m) ? -1.f : 1.f;
 #pragma unroll
-        for (int k = 0; k < 4; k++) {
-            const float o = shfl_xor(v[k], m);
-            v[k] = (lane & m) ? o - v[k] : v[k] + o;
-        }
+        for (int k = 0; k < 4; k++) v[k] = __builtin_fmaf(sg, v[k], shfl_xor(v[k], m));
+    }
 #pragma unroll
     for (int k = 0; k < 4; k++) v[k] *= 0.0625f;
 }
@@ -151,14 +152,8 @@ __device__ __forceinline__ uint16_t f2h_bits(float x) {
 }
 __device__ __forceinline__ float h2f_bits(uint16_t b) { return (float) __builtin_bit_cast(_Float16, b); }
 
-// q8_0 store of one row (kv_store_q8, qwen38_mk.cu:2005-2022): codes of this lane's 4 values as one word, scale of its block
-__device__ __forceinline__ unsigned quant_q8(const float (&v)[4], uint16_t & sc) {
-    float am = 0.f;
-#pragma unroll
-    for (int k = 0; k < 4; k++) am = fmaxf(am, fabsf(v[k]));
-    am = fmaxf(am, shfl_xor(am, 1));
-    am = fmaxf(am, shfl_xor(am, 2));
-    am = fmaxf(am, shfl_xor(am, 4));
+// q8_0 codes of this lane's 4 values as one word and the scale of its block, given the block's max |v| am
+__device__ __forceinline__ unsigned quant_q8_am(const float (&v)[4], float am, uint16_t & sc) {
     const float id = am > 0.f ? 127.0f / am : 0.f;
     unsigned w = 0;
 #pragma unroll
@@ -166,10 +161,21 @@ __device__ __forceinline__ unsigned quant_q8(const float (&v)[4], uint16_t & sc)
     sc = f2h_bits(am / 127.0f);
     return w;
 }
+// max |v| over the lane's 32-value block (8 lanes)
+__device__ __forceinline__ float block_absmax(const float (&v)[4]) {
+    float am = 0.f;
+#pragma unroll
+    for (int k = 0; k < 4; k++) am = fmaxf(am, fabsf(v[k]));
+    am = fmaxf(am, shfl_xor(am, 1));
+    am = fmaxf(am, shfl_xor(am, 2));
+    return fmaxf(am, shfl_xor(am, 4));
+}
+// q8_0 store of one row (kv_store_q8, qwen38_mk.cu:2005-2022): codes of this lane's 4 values as one word, scale of its block
+__device__ __forceinline__ unsigned quant_q8(const float (&v)[4], uint16_t & sc) { return quant_q8_am(v, block_absmax(v), sc); }
 
 // b-bit store (kv_store_q4 :2029-2046 / kv_store_qn :2075-2097): signed max (ties -> larger value), d = sv / -h,
 // id = 1/d, n = min(2h-1, (int) fma(v, id, h + 0.5)).  Returns the 4 codes n (one per byte).
-__device__ __forceinline__ unsigned quant_qn(const float (&v)[4], int bits, uint16_t & sc) {
+__device__ __forceinline__ unsigned quant_qn(const float (&v)[4], int bits, uint16_t & sc, float & amax) {
     const int h = 1 << (bits - 1);
     float am = 0.f, sv = 0.f;
 #pragma unroll
@@ -180,6 +186,7 @@ __device__ __forceinline__ unsigned quant_qn(const float (&v)[4], int bits, uint
         const float oa = shfl_xor(am, m), os = shfl_xor(sv, m);
         if (oa > am || (oa == am && os > sv)) { am = oa; sv = os; }
     }
+    amax = am; // the block's max |v| (the q8 ring copy's)
     const float d = sv / (float) -h, id = d != 0.f ? 1.0f / d : 0.f;
     unsigned codes = 0;
 #pragma unroll
@@ -239,12 +246,14 @@ __device__ __forceinline__ void store_row(const RowGeo & S, const SideLayout & s
     if (sd.rot) fwht256_w64(v);
     const size_t row = main_row(S, seq, g, p);
     uint16_t sc;
+    float am; // the block's max |v|, shared by the main row's quantizer and the ring copy
     if (sd.bits == 8) {
-        const unsigned word = quant_q8(v, sc);
+        am = block_absmax(v);
+        const unsigned word = quant_q8_am(v, am, sc);
         *reinterpret_cast<unsigned *>(sd.vals + row * HD + 4 * lane) = word;
     } else {
         const int bits = sd.bits, hb = bits - 4, odd = lane & 1;
-        const unsigned codes = quant_qn(v, bits, sc);
+        const unsigned codes = quant_qn(v, bits, sc, am);
         // word lane/2 of the row: the even lane's values are its low nibbles, the odd lane's the high nibbles
         unsigned nib = codes & 0x0f0f0f0fu;
         if (odd) nib <<= 4;
@@ -263,7 +272,7 @@ __device__ __forceinline__ void store_row(const RowGeo & S, const SideLayout & s
     if ((lane & 7) == 0) sd.scs[row * 8 + (lane >> 3)] = sc;
     if (ring && sd.ring) {
         uint16_t rs;
-        const unsigned word = quant_q8(v, rs);
+        const unsigned word = quant_q8_am(v, am, rs);
         const size_t rr = ring_row(S, seq, g, p);
         *reinterpret_cast<unsigned *>(sd.ring + rr * HD + 4 * lane) = word;
         if ((lane & 7) == 0) sd.rsc[rr * 8 + (lane >> 3)] = rs;

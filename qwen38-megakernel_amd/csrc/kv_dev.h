@@ -178,13 +178,20 @@ __device__ __forceinline__ unsigned quant_q8(const float (&v)[4], uint16_t & sc)
 __device__ __forceinline__ unsigned quant_qn(const float (&v)[4], int bits, uint16_t & sc, float & amax) {
     const int h = 1 << (bits - 1);
     float am = 0.f, sv = 0.f;
+    // (selects, not branches: the row is one dependent chain per wave)
 #pragma unroll
-    for (int k = 0; k < 4; k++)
-        if (fabsf(v[k]) > am || (fabsf(v[k]) == am && v[k] > sv)) { am = fabsf(v[k]); sv = v[k]; }
+    for (int k = 0; k < 4; k++) {
+        const float a = fabsf(v[k]);
+        const bool take = a > am || (a == am && v[k] > sv);
+        am = take ? a : am;
+        sv = take ? v[k] : sv;
+    }
 #pragma unroll
     for (int m = 1; m <= 4; m <<= 1) {
         const float oa = shfl_xor(am, m), os = shfl_xor(sv, m);
-        if (oa > am || (oa == am && os > sv)) { am = oa; sv = os; }
+        const bool take = oa > am || (oa == am && os > sv);
+        am = take ? oa : am;
+        sv = take ? os : sv;
     }
     amax = am; // the block's max |v| (the q8 ring copy's)
     const float d = sv / (float) -h, id = d != 0.f ? 1.0f / d : 0.f;
@@ -241,10 +248,10 @@ __device__ __forceinline__ void load_row4(const void * in, size_t row, int f16, 
 
 // the row of position p (kv head g of sequence seq) on side sd: optional FWHT, the main row in the side's format and,
 // when ring and the side has a window, the q8 ring copy of the same rotated values.  All 64 lanes call it.
-__device__ __forceinline__ void store_row(const RowGeo & S, const SideLayout & sd, int seq, int g, int p, bool ring, float (&v)[4]) {
+// row: the main-store row of (seq, g, p); rr: its ring row (used when ring)
+__device__ __forceinline__ void store_row_at(const SideLayout & sd, size_t row, size_t rr, bool ring, float (&v)[4]) {
     const int lane = lane_id();
     if (sd.rot) fwht256_w64(v);
-    const size_t row = main_row(S, seq, g, p);
     uint16_t sc;
     float am; // the block's max |v|, shared by the main row's quantizer and the ring copy
     if (sd.bits == 8) {
@@ -273,10 +280,12 @@ __device__ __forceinline__ void store_row(const RowGeo & S, const SideLayout & s
     if (ring && sd.ring) {
         uint16_t rs;
         const unsigned word = quant_q8_am(v, am, rs);
-        const size_t rr = ring_row(S, seq, g, p);
         *reinterpret_cast<unsigned *>(sd.ring + rr * HD + 4 * lane) = word;
         if ((lane & 7) == 0) sd.rsc[rr * 8 + (lane >> 3)] = rs;
     }
+}
+__device__ __forceinline__ void store_row(const RowGeo & S, const SideLayout & sd, int seq, int g, int p, bool ring, float (&v)[4]) {
+    store_row_at(sd, main_row(S, seq, g, p), S.kvrc > 0 ? ring_row(S, seq, g, p) : 0, ring, v);
 }
 
 __device__ __forceinline__ void store_row(const StoreLayout & S, const SideLayout & sd, int seq, int g, int p, bool ring, float (&v)[4]) {

@@ -14,7 +14,9 @@ namespace qkv {
 // One wave per row; lane l holds values 4l .. 4l+3.  Rows of the input: [T][nl][NKV][256] (fp16 or fp32).
 __global__ __launch_bounds__(256) void k_append(StoreLayout S, int seq, int layer0, int nl, int pos, int T, const void * kin,
                                                 const void * vin, int f16, const float * knw, const float2 * rope) {
-    const int wave = blockIdx.x * 4 + (threadIdx.x >> 6);
+    // the row index as a scalar: the side's layout and the page-table entry then come from scalar loads issued at the
+    // start, not from vector loads whose waits would put a memory round trip between each step of the row
+    const int wave = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     if (wave >= T * nl * NKV * 2) return;
     const int w = wave & 1;
     int r = wave >> 1;
@@ -22,13 +24,18 @@ __global__ __launch_bounds__(256) void k_append(StoreLayout S, int seq, int laye
     r /= NKV;
     const int l = r % nl, t = r / nl;
     const size_t src = ((size_t) (t * nl + l) * NKV + g) * HD;
+    const int p = pos + t;
+    // every load the row needs, issued together before the first wait: the input values, the page-table entry of
+    // the main row and the side's layout (scalar loads, made live here by the empty asm)
     float v[4];
     load_row4(w ? vin : kin, src, f16, v);
-    const int p = pos + t;
+    const size_t row = main_row(S, seq, g, p), rr = S.kvrc > 0 ? ring_row(S, seq, g, p) : 0;
+    const SideLayout sd = S.side[layer0 + l][w];
+    asm volatile("" ::"s"(sd.vals), "s"(sd.scs), "s"(sd.ring), "s"(sd.rsc), "s"(sd.bits), "s"(sd.rot));
     if (knw && !w) qk_prep(v, knw + (size_t) l * HD, rope + (size_t) p * 32);
     // ring copy: only for the newest kvrc positions of the call (p >= pos + T - kvrc); an older one shares its ring
     // row with a newer position of the same launch and is evicted by it anyway, and writing both would race
-    store_row(S, S.side[layer0 + l][w], seq, g, p, p >= pos + T - S.kvrc, v);
+    store_row_at(sd, row, rr, p >= pos + T - S.kvrc, v);
 }
 
 // One wave per (position, layer, side, kv head) of positions p0 .. p1-1.

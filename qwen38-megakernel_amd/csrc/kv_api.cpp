@@ -140,7 +140,10 @@ struct Store {
     size_t ml_bytes = 0;
     int max_blocks = 0;
     int occupancy = 0; // decode workgroups per CU: 0 = by launch size, 2 or 3 (launch_attn)
-    int wide = 1;      // 25..48 query rows per kv head: one pass of 8-wave workgroups (1) or two batches of 24 rows (0)
+    // 25..48 query rows per kv head: one pass of 8-wave workgroups (1), two batches of 24 rows (0), or by format (2):
+    // one pass for q8 K and V, two batches for packed sides, whose dequantization done by both waves of a pair makes
+    // the one-pass form the slower one there (preset F at T = 8: 105 vs 94 us per layer; all-q8: 36.7 vs 37.1)
+    int wide = 2;
     // RoPE table of the Q/K prep calls: [rope_rows][32] (cos, sin), the caller's or the store's own text table
     const float2 * rope = nullptr;
     int rope_rows = 0;
@@ -502,7 +505,7 @@ static int attend_impl(void * h, int layer0, int n_layers, int n_seq, const int 
         a.qnw = qnw;
         a.R = GQA * T;
         a.RP = a.R <= 8 ? 8 : a.R <= 16 ? 16 : 24; // T = 1: one 8-row group; T = 2: 16 rows; T >= 3: 24 rows per wave
-        a.wide = a.R > 24 && s.wide;               // T >= 5: both halves of 24 rows in one workgroup
+        a.wide = 0;                                 // (per launch below: T >= 5, by the knob and the launch's formats)
         a.nseq = n_seq;
         int seg_total = 0;
         for (int i = 0; i < n_seq; i++) {
@@ -586,7 +589,8 @@ static int attend_impl(void * h, int layer0, int n_layers, int n_seq, const int 
                 item += b.nl * NKV * b.sd[i].nseg;
             }
             b.n_base = item;
-            b.n_items = item * (a.wide ? 1 : (a.R + a.RP - 1) / a.RP);
+            b.wide = a.R > 24 && (s.wide == 1 || (s.wide == 2 && kb == 8 && vb == 8));
+            b.n_items = item * (b.wide ? 1 : (a.R + a.RP - 1) / a.RP);
             if (!prefetch) {
                 b.q = q + (size_t) l * n_seq * T * NH * qs;
                 b.out = out + (size_t) l * n_seq * T * NH * HD;
@@ -997,7 +1001,7 @@ int mk_kv_config(void * h, const char * key, long long value) {
             return 0;
         }
         if (!strcmp(key, "wide")) {
-            if (value != 0 && value != 1) throw std::runtime_error("wide must be 0 or 1");
+            if (value < 0 || value > 2) throw std::runtime_error("wide must be 0 (two 24-row passes), 1 (one pass) or 2 (by format)");
             s.wide = (int) value;
             return 0;
         }

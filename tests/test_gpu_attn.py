@@ -231,7 +231,9 @@ def test_attend_errors(qkv, torch_gpu):
     with pytest.raises(qkv.KVError, match="occupancy"):
         st.config("occupancy", 1)
     with pytest.raises(qkv.KVError, match="wide"):
-        st.config("wide", 2)
+        st.config("wide", 3)
+    with pytest.raises(qkv.KVError, match="wide"):
+        st.config("wide", -1)
     with pytest.raises(qkv.KVError, match="unknown knob"):
         st.config("no_such_knob", 0)
 

@@ -22,9 +22,14 @@ FLAGS = [
 ]
 
 
+# per-source additions: the append kernel takes its leading scalar arguments preloaded into SGPRs (gfx950 kernel-argument
+# preloading; code objects keep the argument loads for firmware without it)
+EXTRA = {"kv_store.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=14"]}
+
+
 def _compile(src):
     obj = os.path.join(BUILD, os.path.splitext(src)[0] + ".o")
-    cmd = [HIPCC, *FLAGS, "-c", os.path.join(CSRC, src), "-o", obj]
+    cmd = [HIPCC, *FLAGS, *EXTRA.get(src, []), "-c", os.path.join(CSRC, src), "-o", obj]
     if src.endswith(".cpp"):
         cmd.insert(1, "-xhip")
     r = subprocess.run(cmd, capture_output=True, text=True)

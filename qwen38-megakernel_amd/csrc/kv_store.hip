@@ -12,15 +12,15 @@
 namespace qkv {
 
 // One wave per row; lane l holds values 4l .. 4l+3.  Rows of the input: [T][nl][NKV][256] (fp16 or fp32).
-__global__ __launch_bounds__(256) void k_append(StoreLayout S, int seq, int layer0, int nl, int pos, int T, const void * kin,
-                                                const void * vin, int f16, const float * knw, const float2 * rope) {
+// The scalar arguments come first: this file is built with kernel-argument preloading (the first 14 dwords arrive in
+// SGPRs at wave launch), so the input address and the page-table entry's address (ptab, pt_stride, page: copies of
+// S's) need no round trip to the argument segment, and every load of the row issues at once.
+__global__ __launch_bounds__(256) void k_append(int seq, int layer0, int nl, int pos, int T, int f16, const void * kin, const void * vin,
+                                                const int * ptab, int pt_stride, int page, StoreLayout S, const float * knw,
+                                                const float2 * rope) {
     // the row index as a scalar: the side's layout and the page-table entry then come from scalar loads issued at the
     // start, not from vector loads whose waits would put a memory round trip between each step of the row
     const int wave = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    // the arguments the input address needs, in one round of scalar loads (not one round before the bounds check and
-    // another after it)
-    asm volatile("" ::"s"(T), "s"(nl), "s"(pos), "s"(kin), "s"(vin), "s"(f16), "s"(S.ptab), "s"(S.pt_stride), "s"(S.page), "s"(S.n_pages),
-                 "s"(S.kvrc));
     if (wave >= T * nl * NKV * 2) return;
     const int w = wave & 1;
     int r = wave >> 1;
@@ -29,36 +29,32 @@ __global__ __launch_bounds__(256) void k_append(StoreLayout S, int seq, int laye
     const int l = r % nl, t = r / nl;
     const size_t src = ((size_t) (t * nl + l) * NKV + g) * HD;
     const int p = pos + t;
-    // every load the row needs, issued before the first wait: the input values, then the page-table entry of the main
-    // row and the side's layout (scalar loads, made live by the empty asm while the input load is in flight)
-    const void * in = w ? vin : kin;
-    uint4 raw; // the lane's 4 values as loaded (fp16: the first 8 bytes)
-    if (f16) {
-        const uint2 x = *reinterpret_cast<const uint2 *>(static_cast<const _Float16 *>(in) + src + 4 * lane_id());
-        raw = make_uint4(x.x, x.y, 0u, 0u);
-    } else {
-        raw = *reinterpret_cast<const uint4 *>(static_cast<const float *>(in) + src + 4 * lane_id());
-    }
-    // (the page-table entry through the constant address space: a scalar load; no kernel writes the table)
-    const int lp = p / S.page;
-    const int phys = ((const __attribute__((address_space(4))) int *) S.ptab)[seq * S.pt_stride + lp];
-    const size_t row = (size_t) (g * S.n_pages + phys) * S.page + (p - lp * S.page);
-    const size_t rr = S.kvrc > 0 ? ring_row(S, seq, g, p) : 0;
+    // every load the row needs, issued before the first wait: the page-table entry of the main row and the side's
+    // layout (scalar loads; the page table through the constant address space: no kernel writes it), and the input
+    // values; the empty asm after the input load makes the scalar values live while that load is in flight
+    const int lp = p / page;
+    const int phys = ((const __attribute__((address_space(4))) int *) ptab)[seq * pt_stride + lp];
     const SideLayout sd = S.side[layer0 + l][w];
-    asm volatile("" ::"s"(sd.vals), "s"(sd.scs), "s"(sd.ring), "s"(sd.rsc), "s"(sd.bits), "s"(sd.rot));
+    const void * in = w ? vin : kin;
     float v[4];
     if (f16) {
-        const half2v a = __builtin_bit_cast(half2v, raw.x), b = __builtin_bit_cast(half2v, raw.y);
+        const uint2 x = *reinterpret_cast<const uint2 *>(static_cast<const _Float16 *>(in) + src + 4 * lane_id());
+        asm volatile("" ::"s"(phys), "s"(sd.vals), "s"(sd.scs), "s"(sd.ring), "s"(sd.rsc), "s"(sd.bits), "s"(sd.rot), "s"(S.n_pages), "s"(S.kvrc));
+        const half2v a = __builtin_bit_cast(half2v, x.x), b = __builtin_bit_cast(half2v, x.y);
         v[0] = (float) a[0];
         v[1] = (float) a[1];
         v[2] = (float) b[0];
         v[3] = (float) b[1];
     } else {
-        v[0] = __builtin_bit_cast(float, raw.x);
-        v[1] = __builtin_bit_cast(float, raw.y);
-        v[2] = __builtin_bit_cast(float, raw.z);
-        v[3] = __builtin_bit_cast(float, raw.w);
+        const float4 x = *reinterpret_cast<const float4 *>(static_cast<const float *>(in) + src + 4 * lane_id());
+        asm volatile("" ::"s"(phys), "s"(sd.vals), "s"(sd.scs), "s"(sd.ring), "s"(sd.rsc), "s"(sd.bits), "s"(sd.rot), "s"(S.n_pages), "s"(S.kvrc));
+        v[0] = x.x;
+        v[1] = x.y;
+        v[2] = x.z;
+        v[3] = x.w;
     }
+    const size_t row = (size_t) (g * S.n_pages + phys) * page + (p - lp * page);
+    const size_t rr = S.kvrc > 0 ? ring_row(S, seq, g, p) : 0;
     if (knw && !w) qk_prep(v, knw + (size_t) l * HD, rope + (size_t) p * 32);
     // ring copy: only for the newest kvrc positions of the call (p >= pos + T - kvrc); an older one shares its ring
     // row with a newer position of the same launch and is evicted by it anyway, and writing both would race
@@ -108,8 +104,8 @@ __global__ __launch_bounds__(256) void k_ring_refill(StoreLayout S, int seq, int
 hipError_t launch_append(const StoreLayout & S, int seq, int layer0, int nl, int pos, int T, const void * k, const void * v, int f16,
                          hipStream_t st, hipEvent_t ev0, hipEvent_t ev1, const float * knw, const float2 * rope) {
     const int waves = T * nl * NKV * 2;
-    hipExtLaunchKernelGGL(k_append, dim3((waves + 3) / 4), dim3(256), 0, st, ev0, ev1, 0, S, seq, layer0, nl, pos, T, k, v, f16, knw,
-                          rope);
+    hipExtLaunchKernelGGL(k_append, dim3((waves + 3) / 4), dim3(256), 0, st, ev0, ev1, 0, seq, layer0, nl, pos, T, f16, k, v, S.ptab,
+                          S.pt_stride, S.page, S, knw, rope);
     return hipGetLastError();
 }
 

@@ -240,12 +240,18 @@ __device__ __forceinline__ void vcodes_word(const VRaw<B> & v, int j, int w, uns
 // these copies set it in this kernel.
 // Stage layout (STAGE_BYTES, one per wave and stage): K rows [32][32 KB], V rows [32][32 VB], K scales [32][8],
 // V scales [32][8] (fp16).  Rows past the end of the context are copies of the last row (finite, masked later).
+// The copies carry the non-temporal hint (nt): each tile is read once, so it is streamed through the L2 without
+// displacing what is read again (code, kernel arguments, page tables, the partials the combine reads).  Measured on
+// configs 3 and 5: 1-2% shorter steps, the same bits.
+#ifndef QKV_DMA_CPOL
+#define QKV_DMA_CPOL " nt"
+#endif
 __device__ __forceinline__ void dma16(const void * g, unsigned lds) {
-    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds), "v"(g) : "memory");
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" QKV_DMA_CPOL ::"s"(lds), "v"(g) : "memory");
 }
 // the same with a scalar base address and a 32-bit per-lane byte offset (no 64-bit vector address per copy)
 __device__ __forceinline__ void dma16s(const void * base, unsigned voff, unsigned lds) {
-    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds), "v"(voff), "s"(base) : "memory");
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" QKV_DMA_CPOL ::"s"(lds), "v"(voff), "s"(base) : "memory");
 }
 __device__ __forceinline__ void lds_drain() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 // a workgroup barrier for LDS data only: __syncthreads() also waits for every vector-memory operation of the wave,

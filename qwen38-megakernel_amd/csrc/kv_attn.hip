@@ -332,16 +332,16 @@ __device__ __forceinline__ void pq_issue(const TileSrc & t, int nq, unsigned lds
     for (int j = 0; j < 2; j++) {
         int o = 1024 * j + 16 * lane;
         if (o >= nq * KRB) o = nq * KRB - 16;
-        dma16(t.k + o, lds + 1024 * j);
+        dma16_keep(t.k + o, lds + 1024 * j);
     }
 #pragma unroll
     for (int j = 0; j < 2; j++) {
         int o = 1024 * j + 16 * lane;
         if (o >= nq * VRB) o = nq * VRB - 16;
-        dma16(t.v + o, lds + 2048 + 1024 * j);
+        dma16_keep(t.v + o, lds + 2048 + 1024 * j);
     }
     const int r = min(lane & 7, nq - 1);
-    dma16(lane < 8 ? static_cast<const void *>(t.ks + 8 * r) : static_cast<const void *>(t.vs + 8 * r), lds + 4096);
+    dma16_keep(lane < 8 ? static_cast<const void *>(t.ks + 8 * r) : static_cast<const void *>(t.vs + 8 * r), lds + 4096);
 }
 
 // one producer lane: position lane % 8 of its quarter, scale block lane / 8, K and V into the fp16 buffer

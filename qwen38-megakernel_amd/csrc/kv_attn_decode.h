@@ -246,12 +246,32 @@ __device__ __forceinline__ void vcodes_word(const VRaw<B> & v, int j, int w, uns
 #ifndef QKV_DMA_CPOL
 #define QKV_DMA_CPOL " nt"
 #endif
+// NT = false: without the hint, for tiles that other work items read again (prefill row blocks of one key segment,
+// the row batches of one decode segment)
+// the LDS address and the base are wave-uniform; readfirstlane keeps them in SGPRs wherever the compiler placed them
+template <bool NT = true>
 __device__ __forceinline__ void dma16(const void * g, unsigned lds) {
-    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" QKV_DMA_CPOL ::"s"(lds), "v"(g) : "memory");
+    const unsigned m = (unsigned) __builtin_amdgcn_readfirstlane((int) lds);
+    if constexpr (NT) asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" QKV_DMA_CPOL ::"s"(m), "v"(g) : "memory");
+    else asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(m), "v"(g) : "memory");
 }
+__device__ __forceinline__ void dma16_keep(const void * g, unsigned lds) { dma16<false>(g, lds); }
 // the same with a scalar base address and a 32-bit per-lane byte offset (no 64-bit vector address per copy)
+template <bool NT = true>
 __device__ __forceinline__ void dma16s(const void * base, unsigned voff, unsigned lds) {
-    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" QKV_DMA_CPOL ::"s"(lds), "v"(voff), "s"(base) : "memory");
+    const unsigned m = (unsigned) __builtin_amdgcn_readfirstlane((int) lds);
+    const size_t x = (size_t) base;
+    const unsigned lo = (unsigned) __builtin_amdgcn_readfirstlane((int) (unsigned) x), hi = (unsigned) __builtin_amdgcn_readfirstlane((int) (x >> 32));
+    const void * const b = (const void *) (((size_t) hi << 32) | lo);
+    if constexpr (NT)
+        asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" QKV_DMA_CPOL ::"s"(m), "v"(voff), "s"(b) : "memory");
+    else asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(m), "v"(voff), "s"(b) : "memory");
+}
+// a segment partial's four values, stored with the non-temporal hint: the combine reads them from beyond the L2 of the
+// XCD that wrote them (configs 3 fused, 4, 5: 1-2% shorter launches, the same bits)
+__device__ __forceinline__ void store_part(float * p, const float4 & y) {
+    typedef float f4v __attribute__((ext_vector_type(4)));
+    __builtin_nontemporal_store(f4v{y.x, y.y, y.z, y.w}, reinterpret_cast<f4v *>(p));
 }
 __device__ __forceinline__ void lds_drain() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 // a workgroup barrier for LDS data only: __syncthreads() also waits for every vector-memory operation of the wave,
@@ -309,7 +329,7 @@ __device__ __forceinline__ TileSrc tile_src(const StoreLayout & S, const SideLay
 // 16-byte chunk to the last valid row.
 // PART: 0 = the whole tile, 1 = the K rows and scales, 2 = the V rows and scales (two waves sharing one stage, each
 // copying what it stores in a fused append)
-template <int KB, int VB, int PART = 0>
+template <int KB, int VB, int PART = 0, bool NT = true>
 __device__ __forceinline__ void issue_tile(const TileSrc & t, int nv, unsigned lds, int lane) {
     constexpr int KR = 2 * KB, VR = 2 * VB; // 16-byte chunks per row
     constexpr bool DK = PART != 2, DV = PART != 1;
@@ -317,10 +337,10 @@ __device__ __forceinline__ void issue_tile(const TileSrc & t, int nv, unsigned l
         const unsigned off = 16 * lane;
         if constexpr (DK)
 #pragma unroll
-            for (int j = 0; j < KB; j++) dma16s(t.k + 1024 * j, off, lds + 1024 * j);
+            for (int j = 0; j < KB; j++) dma16s<NT>(t.k + 1024 * j, off, lds + 1024 * j);
         if constexpr (DV)
 #pragma unroll
-            for (int j = 0; j < VB; j++) dma16s(t.v + 1024 * j, off, lds + 1024 * (KB + j));
+            for (int j = 0; j < VB; j++) dma16s<NT>(t.v + 1024 * j, off, lds + 1024 * (KB + j));
     } else {
         if constexpr (DK)
 #pragma unroll
@@ -328,7 +348,7 @@ __device__ __forceinline__ void issue_tile(const TileSrc & t, int nv, unsigned l
                 int c = j * 64 + lane;
                 const int r = c / KR;
                 if (r >= nv) c = (nv - 1) * KR + (c - r * KR);
-                dma16(t.k + 16 * c, lds + 1024 * j);
+                dma16<NT>(t.k + 16 * c, lds + 1024 * j);
             }
         if constexpr (DV)
 #pragma unroll
@@ -336,38 +356,38 @@ __device__ __forceinline__ void issue_tile(const TileSrc & t, int nv, unsigned l
                 int c = j * 64 + lane;
                 const int r = c / VR;
                 if (r >= nv) c = (nv - 1) * VR + (c - r * VR);
-                dma16(t.v + 16 * c, lds + 1024 * (KB + j));
+                dma16<NT>(t.v + 16 * c, lds + 1024 * (KB + j));
             }
     }
     const int r = min(lane & 31, nv - 1);
     if constexpr (PART == 0) {
-        dma16(lane < 32 ? static_cast<const void *>(t.ks + 8 * r) : static_cast<const void *>(t.vs + 8 * r), lds + 1024 * (KB + VB));
+        dma16<NT>(lane < 32 ? static_cast<const void *>(t.ks + 8 * r) : static_cast<const void *>(t.vs + 8 * r), lds + 1024 * (KB + VB));
     } else if ((lane < 32) == (PART == 1)) { // half the lanes: the same LDS slots (lane-indexed) as the whole copy
-        dma16(PART == 1 ? static_cast<const void *>(t.ks + 8 * r) : static_cast<const void *>(t.vs + 8 * r), lds + 1024 * (KB + VB));
+        dma16<NT>(PART == 1 ? static_cast<const void *>(t.ks + 8 * r) : static_cast<const void *>(t.vs + 8 * r), lds + 1024 * (KB + VB));
     }
 }
 
 // a q8 tile through a stage smaller than one (three workgroups per CU): part 0 = the K rows at 0 and every scale at
 // 8 KiB, part 1 = the V rows at 0 once the K operands are in registers; partial tiles clamp as issue_tile does
-template <int PART>
+template <int PART, bool NT = true>
 __device__ __forceinline__ void issue_q8_part(const TileSrc & t, int nv, unsigned lds, int lane) {
     const uint8_t * const src = PART == 0 ? t.k : t.v;
     if (nv == ATP) {
         const unsigned off = 16 * lane;
 #pragma unroll
-        for (int j = 0; j < 8; j++) dma16s(src + 1024 * j, off, lds + 1024 * j);
+        for (int j = 0; j < 8; j++) dma16s<NT>(src + 1024 * j, off, lds + 1024 * j);
     } else {
 #pragma unroll
         for (int j = 0; j < 8; j++) {
             int c = j * 64 + lane;
             const int r = c / 16;
             if (r >= nv) c = (nv - 1) * 16 + (c - r * 16);
-            dma16(src + 16 * c, lds + 1024 * j);
+            dma16<NT>(src + 16 * c, lds + 1024 * j);
         }
     }
     if constexpr (PART == 0) {
         const int r = min(lane & 31, nv - 1);
-        dma16(lane < 32 ? static_cast<const void *>(t.ks + 8 * r) : static_cast<const void *>(t.vs + 8 * r), lds + 8192);
+        dma16<NT>(lane < 32 ? static_cast<const void *>(t.ks + 8 * r) : static_cast<const void *>(t.vs + 8 * r), lds + 8192);
     }
 }
 
@@ -847,7 +867,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SMALL ? 3 :
             const TileSrc t = tile_src<KB, VB>(S, SK, SV, g, p0, phys, ring0, ring);
             int ln = lane; // opaque: the per-lane chunk addresses are not hoisted out of the tile loop into registers
             asm volatile("" : "+v"(ln));
-            if (ring) {
+            if (nb > 1) { // the item's other row batches stream the same tiles: no non-temporal hint
+                if (ring) {
+                    if constexpr (SMALL) issue_q8_part<0, false>(t, nv, lds_to, ln);
+                    else issue_tile<8, 8, 0, false>(t, nv, lds_to, ln);
+                } else {
+                    issue_tile<KB, VB, 0, false>(t, nv, lds_to, ln);
+                }
+            } else if (ring) {
                 if constexpr (SMALL) issue_q8_part<0>(t, nv, lds_to, ln);
                 else issue_tile<8, 8>(t, nv, lds_to, ln);
             } else {
@@ -1079,7 +1106,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SMALL ? 3 :
                     y.z += z.z;
                     y.w += z.w;
                 }
-                *reinterpret_cast<float4 *>(a.part + ((size_t) item * R + row0 + 16 * ps + r16) * HD + 4 * c4) = y;
+                store_part(a.part + ((size_t) item * R + row0 + 16 * ps + r16) * HD + 4 * c4, y);
             }
             if (ps + 1 < NPASS) __syncthreads();
         }
@@ -1340,7 +1367,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                     y.z += z.z;
                     y.w += z.w;
                 }
-                *reinterpret_cast<float4 *>(a.part + ((size_t) item * R + trow0 + 8 * h + r8) * HD + 4 * c4) = y;
+                store_part(a.part + ((size_t) item * R + trow0 + 8 * h + r8) * HD + 4 * c4, y);
             }
             if (h + 1 < NP) lds_barrier();
         }

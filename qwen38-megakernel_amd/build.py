@@ -24,7 +24,9 @@ FLAGS = [
 
 # per-source additions: the append kernel takes its leading scalar arguments preloaded into SGPRs (gfx950 kernel-argument
 # preloading; code objects keep the argument loads for firmware without it)
-EXTRA = {"kv_store.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=14"]}
+# and so do the one-sequence combine kernel's seven scalar arguments (kernels whose first argument is a struct preload
+# nothing)
+EXTRA = {"kv_store.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=14"], "kv_attn.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=7"]}
 
 
 def _compile(src):

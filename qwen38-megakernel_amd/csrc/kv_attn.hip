@@ -175,13 +175,14 @@ __device__ __forceinline__ void combine_row(const AttnArgs & a, const CombineRow
     }
 }
 
-__device__ __forceinline__ void combine_split(const AttnArgs & a, const CombineRow & cr, int dq, uint8_t * scratch) {
+// one (row, 64-dim quarter dq) of the output from the row's segment partials; part / ml / out as in AttnArgs, nseg and
+// item0 those of the row's sequence si
+__device__ __forceinline__ void combine_split_core(const float * __restrict__ part, const float2 * __restrict__ ml_, float * out, int R, int T,
+                                                   int nseq, int nseg, int item0, const CombineRow & cr, int dq, uint8_t * scratch) {
     float4 (*s_num)[16] = reinterpret_cast<float4 (*)[16]>(scratch);        // [AWAVES][16]
     float2 * s_md = reinterpret_cast<float2 *>(scratch + AWAVES * 16 * 16); // [AWAVES]
-    const int R = a.R, T = a.T, r = cr.r, g = cr.g, si = cr.si, l = cr.l;
-    const SeqDesc & sd = a.sd[si];
-    const int nseg = sd.nseg;
-    const size_t head0 = (size_t) sd.item0 + (size_t) (l * NKV + g) * nseg;
+    const int r = cr.r, g = cr.g, si = cr.si, l = cr.l;
+    const size_t head0 = (size_t) item0 + (size_t) (l * NKV + g) * nseg;
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, sub = lane >> 4, dl = lane & 15;
     const int slot = 4 * wv + sub, dim = 64 * dq + 4 * dl;
     constexpr int PER = MAX_SEG / 16;
@@ -191,8 +192,8 @@ __device__ __forceinline__ void combine_split(const AttnArgs & a, const CombineR
     for (int k = 0; k < PER; k++) {
         const int c = slot + 16 * k;
         if (c < nseg) {
-            ml[k] = a.ml[(head0 + c) * R + r];
-            o[k] = *reinterpret_cast<const float4 *>(a.part + ((head0 + c) * R + r) * HD + dim);
+            ml[k] = ml_[(head0 + c) * R + r];
+            o[k] = *reinterpret_cast<const float4 *>(part + ((head0 + c) * R + r) * HD + dim);
         }
     }
     float Ms = -INFINITY;
@@ -241,7 +242,7 @@ __device__ __forceinline__ void combine_split(const AttnArgs & a, const CombineR
             dd = __builtin_fmaf(e, md.y, dd);
         }
         const int h = GQA * g + r / T, t = r % T;
-        *reinterpret_cast<float4 *>(a.out + (((size_t) (l * a.nseq + si) * T + t) * NH + h) * HD + dim) =
+        *reinterpret_cast<float4 *>(out + (((size_t) (l * nseq + si) * T + t) * NH + h) * HD + dim) =
             make_float4(y.x / dd, y.y / dd, y.z / dd, y.w / dd);
     }
 }
@@ -253,7 +254,23 @@ __global__ __launch_bounds__(256) void k_combine(AttnArgs a) {
 
 __global__ __launch_bounds__(256) void k_combine_split(AttnArgs a) {
     __shared__ __attribute__((aligned(16))) uint8_t scratch[AWAVES * 16 * 16 + AWAVES * 8];
-    combine_split(a, combine_row_of(a, blockIdx.x >> 2), blockIdx.x & 3, scratch);
+    const CombineRow cr = combine_row_of(a, blockIdx.x >> 2);
+    const SeqDesc & sd = a.sd[cr.si];
+    combine_split_core(a.part, a.ml, a.out, a.R, a.T, a.nseq, sd.nseg, sd.item0, cr, blockIdx.x & 3, scratch);
+}
+
+// the same for one sequence, with every argument a scalar: they arrive preloaded in SGPRs (kernel-argument preloading,
+// build flags of this file), so the partials' loads issue without a round trip to the argument segment first
+__global__ __launch_bounds__(256) void k_combine_split1(const float * part, const float2 * ml, float * out, int R, int T, int nseg, int item0) {
+    __shared__ __attribute__((aligned(16))) uint8_t scratch[AWAVES * 16 * 16 + AWAVES * 8];
+    int b = blockIdx.x >> 2;
+    CombineRow cr;
+    cr.r = b % R;
+    b /= R;
+    cr.g = b % NKV;
+    cr.si = 0;
+    cr.l = b / NKV;
+    combine_split_core(part, ml, out, R, T, 1, nseg, item0, cr, blockIdx.x & 3, scratch);
 }
 
 // launches whose rows need the whole row in one workgroup (V stored rotated, gate, o_proj units) use the row form
@@ -265,6 +282,9 @@ static bool host_combine_needs_rows(const AttnArgs & a) {
 hipError_t launch_combine(const AttnArgs & a, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {
     const unsigned rows = (unsigned) (a.nl * a.nseq * NKV * a.R);
     if (host_combine_needs_rows(a)) hipExtLaunchKernelGGL(k_combine, dim3(rows), dim3(256), 0, st, ev0, ev1, 0, a);
+    else if (a.nseq == 1)
+        hipExtLaunchKernelGGL(k_combine_split1, dim3(4 * rows), dim3(256), 0, st, ev0, ev1, 0, (const float *) a.part, (const float2 *) a.ml, a.out,
+                              a.R, a.T, a.sd[0].nseg, a.sd[0].item0);
     else hipExtLaunchKernelGGL(k_combine_split, dim3(4 * rows), dim3(256), 0, st, ev0, ev1, 0, a);
     return hipGetLastError();
 }

@@ -248,24 +248,20 @@ __device__ __forceinline__ void vcodes_word(const VRaw<B> & v, int j, int w, uns
 #endif
 // NT = false: without the hint, for tiles that other work items read again (prefill row blocks of one key segment,
 // the row batches of one decode segment)
-// the LDS address and the base are wave-uniform; readfirstlane keeps them in SGPRs wherever the compiler placed them
+// NT = false: without the hint, for tiles that other work items read again (prefill row blocks of one key segment,
+// the row batches of one decode segment)
 template <bool NT = true>
 __device__ __forceinline__ void dma16(const void * g, unsigned lds) {
-    const unsigned m = (unsigned) __builtin_amdgcn_readfirstlane((int) lds);
-    if constexpr (NT) asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" QKV_DMA_CPOL ::"s"(m), "v"(g) : "memory");
-    else asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(m), "v"(g) : "memory");
+    if constexpr (NT) asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" QKV_DMA_CPOL ::"s"(lds), "v"(g) : "memory");
+    else asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds), "v"(g) : "memory");
 }
 __device__ __forceinline__ void dma16_keep(const void * g, unsigned lds) { dma16<false>(g, lds); }
 // the same with a scalar base address and a 32-bit per-lane byte offset (no 64-bit vector address per copy)
 template <bool NT = true>
 __device__ __forceinline__ void dma16s(const void * base, unsigned voff, unsigned lds) {
-    const unsigned m = (unsigned) __builtin_amdgcn_readfirstlane((int) lds);
-    const size_t x = (size_t) base;
-    const unsigned lo = (unsigned) __builtin_amdgcn_readfirstlane((int) (unsigned) x), hi = (unsigned) __builtin_amdgcn_readfirstlane((int) (x >> 32));
-    const void * const b = (const void *) (((size_t) hi << 32) | lo);
     if constexpr (NT)
-        asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" QKV_DMA_CPOL ::"s"(m), "v"(voff), "s"(b) : "memory");
-    else asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(m), "v"(voff), "s"(b) : "memory");
+        asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" QKV_DMA_CPOL ::"s"(lds), "v"(voff), "s"(base) : "memory");
+    else asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds), "v"(voff), "s"(base) : "memory");
 }
 // a segment partial's four values, stored with the non-temporal hint: the combine reads them from beyond the L2 of the
 // XCD that wrote them (configs 3 fused, 4, 5: 1-2% shorter launches, the same bits)
@@ -867,18 +863,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SMALL ? 3 :
             const TileSrc t = tile_src<KB, VB>(S, SK, SV, g, p0, phys, ring0, ring);
             int ln = lane; // opaque: the per-lane chunk addresses are not hoisted out of the tile loop into registers
             asm volatile("" : "+v"(ln));
-            if (nb > 1) { // the item's other row batches stream the same tiles: no non-temporal hint
-                if (ring) {
-                    if constexpr (SMALL) issue_q8_part<0, false>(t, nv, lds_to, ln);
-                    else issue_tile<8, 8, 0, false>(t, nv, lds_to, ln);
-                } else {
-                    issue_tile<KB, VB, 0, false>(t, nv, lds_to, ln);
-                }
-            } else if (ring) {
-                if constexpr (SMALL) issue_q8_part<0>(t, nv, lds_to, ln);
-                else issue_tile<8, 8>(t, nv, lds_to, ln);
+            // 24-row kernels (NP = 3) run T = 5..8 as two row batches that stream the same tiles: no non-temporal hint
+            constexpr bool NT = NP < 3;
+            if (ring) {
+                if constexpr (SMALL) issue_q8_part<0, NT>(t, nv, lds_to, ln);
+                else issue_tile<8, 8, 0, NT>(t, nv, lds_to, ln);
             } else {
-                issue_tile<KB, VB>(t, nv, lds_to, ln);
+                issue_tile<KB, VB, 0, NT>(t, nv, lds_to, ln);
             }
         };
 

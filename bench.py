@@ -4,7 +4,9 @@
 Headline (`value`): the 101,600-context workload -- single-query decode attention at 101,600 context, preset F (K 5-bit
 Hadamard-rotated, V 6-bit, 2,048-position q8 window; the reference's window rule puts 3,040 positions in the ring and
 98,560 in the packed store), 16 layers x 4 kv heads x head_dim 256, 24 query heads.  One step = the 16 layers'
-attention (16 attend calls, one per layer, as a decoder issues them), inputs resident in HBM.
+attention (16 attend calls, one per layer, as a decoder issues them, captured once as a HIP graph and replayed, as a
+serving loop issues a decode step; every kernel of every call runs), inputs resident in HBM.  The same calls issued
+one by one from Python are reported too (extra.cfg3.eager_*).
 value = KV positions/s = 16 * 101,600 / step time.
 
 Also measured (in "extra"): config 1 (q8, 4,096 positions), config 2 (append: 8 positions x 16 layers per step,
@@ -190,7 +192,11 @@ def bench_cfg3(torch, qkv, steps, warmup):
     ok = bool(torch.isfinite(out).all().item())
     return {
         "L": L, "ws": ws, "ring_positions": L - ws, "layers": nl,
-        "step_s": t_layers, "positions_per_s": nl * L / t_layers, "gbps": nl * per_layer_bytes / t_layers / 1e9,
+        # the headline step: the 16 one-layer calls replayed from one captured HIP graph (every kernel of every call
+        # runs; the host's per-call launch cost is not in it), as config 2's us_per_step; eager_*: one library call
+        # per layer from Python
+        "step_s": t_graph, "positions_per_s": nl * L / t_graph, "gbps": nl * per_layer_bytes / t_graph / 1e9,
+        "eager_step_s": t_layers, "eager_positions_per_s": nl * L / t_layers, "eager_gbps": nl * per_layer_bytes / t_layers / 1e9,
         "attn_kernel_avg_s": attn_avg, "attn_kernel_bytes": per_layer_bytes,
         "attn_kernel_gbps": per_layer_bytes / attn_avg / 1e9,
         "combine_avg_s": prof["combine_ms"] / calls * 1e-3, "profiled_step_s": prof["step_s"],

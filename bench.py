@@ -237,6 +237,9 @@ def bench_cfg2(torch, qkv, nsteps=512):
     g.manual_seed(2)
     k = torch.randn(nsteps, 8, nl, NKV, HD, device="cuda", dtype=torch.float16, generator=g)
     v = torch.randn(nsteps, 8, nl, NKV, HD, device="cuda", dtype=torch.float16, generator=g)
+    for h in range(NKV):  # 4 outlier channels per kv head scaled x12 (the workload's K distribution)
+        ch = torch.from_numpy(np.random.default_rng(1000 + h).choice(HD, 4, replace=False)).cuda()
+        k[:, :, :, h, ch] *= 12.0
     kp, vp, stride = k.data_ptr(), v.data_ptr(), k[0].numel() * 2
 
     def run(stream=0):
@@ -335,6 +338,16 @@ def bench_prefill(torch, qkv, steps, warmup):
             "attn_tflops": flops / t / 1e12, "finite": bool(torch.isfinite(out).all().item())}
 
 
+def host_threads():
+    """Host threads for the CPU baseline: every CPU this process may run on (its affinity mask), capped by the
+    box's CPU share when OMP_NUM_THREADS states one (16 per GPU on the GPU boxes), and by the oracle's 64."""
+    n = len(os.sched_getaffinity(0))
+    share = os.environ.get("OMP_NUM_THREADS", "")
+    if share.isdigit() and int(share) > 0:
+        n = min(n, int(share))
+    return max(1, min(64, n))
+
+
 def cpu_baseline(qkv, seconds=10.0):
     """The oracle (kv_oracle.c, the reference's split-K arithmetic restated in C) on host cores: layer 0 of config 3
     (101,600 positions, 4 kv heads, 24 query heads, T = 1) on dequantized operands, repeated for ~`seconds`."""
@@ -342,7 +355,7 @@ def cpu_baseline(qkv, seconds=10.0):
     if not os.path.exists(o.LIB):
         from oracle import build
         build.build()
-    threads = max(1, min(16, os.cpu_count() or 1))
+    threads = host_threads()
     L, win = 101600, 2048
     ws = qkv.window_start(L, win)
     rng = np.random.default_rng(3)
@@ -365,6 +378,7 @@ def cpu_baseline(qkv, seconds=10.0):
         if el >= seconds:
             break
     return {"value": L * n / el, "unit": "KV positions/s", "cores": threads, "kind": "port",
+            "host_cpus": len(os.sched_getaffinity(0)), "cpu_share": os.environ.get("OMP_NUM_THREADS"),
             "sample": f"layer 0 of config 3 (101,600 positions, ws {ws}, 4 kv heads x 6 query rows, T=1) on dequantized "
                       f"fp16-valued operands, {n} repetitions in {el:.1f} s with {threads} threads (kv_oracle.c)"}
 
@@ -373,7 +387,7 @@ def cpu_extras(seconds=3.0):
     """The oracle on host cores for config 1 (q8 attention over 4,096 positions, 4 kv heads x 6 rows) and config 2
     (one append step: 16 layers x 4 kv heads x 8 positions x K/V rows, FWHT on K, K 5-bit + V 6-bit + q8 ring copies)."""
     from oracle import oracle as o
-    threads = max(1, min(16, os.cpu_count() or 1))
+    threads = host_threads()
     rng = np.random.default_rng(0)
     L = 4096
     K = np.stack([o.dequant_rows(*o.store_rows(rng.standard_normal((L, HD)).astype(np.float32), 0, 8, ring=False)[:2], 8)

@@ -172,17 +172,21 @@ struct Store {
             for (hipEvent_t e : es.e)
                 if (e) (void) hipEventDestroy(e);
         for (void * p : allocs) (void) hipFree(p);
+        for (void * p : retired) (void) hipFree(p);
         if (part) (void) hipFree(part);
         if (ml) (void) hipFree(ml);
         if (rope_own) (void) hipFree(rope_own);
     }
+    // Workspace buffers a larger call has replaced.  They stay allocated until the store is freed: work already
+    // enqueued, and any HIP graph captured over an earlier call, still hold their addresses (a graph replays the raw
+    // kernel arguments), so freeing them here would let a later replay read and write freed device memory.
+    std::vector<void *> retired;
     void grow(void *& p, size_t & have, size_t need) {
         if (need <= have) return;
-        HCK(hipDeviceSynchronize()); // the old buffer may still be read by enqueued work
-        if (p) HCK(hipFree(p));
-        p = nullptr;
-        have = 0;
-        HCK(hipMalloc(&p, need));
+        void * q = nullptr;
+        HCK(hipMalloc(&q, need));
+        if (p) retired.push_back(p);
+        p = q;
         have = need;
     }
     size_t main_row(int seq, int g, int p) const {

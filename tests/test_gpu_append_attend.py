@@ -21,6 +21,7 @@ def step_inputs(rng, nseq, T, nl):
     ("K*=5r,V*=6", 2048, [20000], 1, 1, True, 0),        # several tiles per wave, the new row in the last ring tile
     ("K*=5r,V*=6", 2048, [40], 1, 2, False, 0),          # a short context: the new row in a wave's first tile
     ("", 0, [1027], 8, 1, True, 0),                      # T = 8 (8-wave kernel), rows 1019..1026 straddle segment 1024
+    ("K*=5r,V*=6", 2048, [20000], 8, 1, True, 0),        # T = 8 on packed sides: two 24-row batches both store the rows
     ("K0=4r,V0=7r,K1=8,V1=5", 640, [3190], 3, 2, False, 0),
     ("K*=5r,V*=6", 1024, [2300, 700, 3100], 2, 1, True, 256),
 ])

@@ -95,7 +95,16 @@ def traffic_from_profiles(name):
         return None
 
 
-def bench_cfg3(torch, qkv, steps, warmup):
+def rocprof_duration(name):
+    """Mean launch duration (µs) of the dominant kernel in the committed rocprofv3 kernel trace, if present."""
+    try:
+        with open(os.path.join(ROOT, "profiles", name)) as f:
+            return json.load(f).get("mean_us")
+    except (OSError, ValueError):
+        return None
+
+
+def bench_cfg3(torch, qkv, steps, warmup, step_only=False):
     L, nl, win = 101600, 16, 2048
     st = qkv.KVStore("K*=5r,V*=6", win=win, n_layers=nl, ctx=L)
     gen_fill(torch, st, 0, L, nl, seed=3, outliers=True)
@@ -132,6 +141,11 @@ def bench_cfg3(torch, qkv, steps, warmup):
             for l in range(nl):
                 st.attend(l, 1, [0], [L], 1, qp + l * lay, op + l * lay, stream=side.cuda_stream)
     t_graph = timed(torch, graph.replay, steps, warmup)
+    if step_only:  # (the profiling run: only the headline's one-layer launches)
+        return {"L": L, "ws": ws, "layers": nl, "step_s": t_graph, "positions_per_s": nl * L / t_graph,
+                "gbps": nl * per_layer_bytes / t_graph / 1e9, "eager_step_s": t_layers, "attn_kernel_avg_s": attn_avg,
+                "attn_kernel_bytes": per_layer_bytes, "attn_kernel_gbps": per_layer_bytes / attn_avg / 1e9,
+                "combine_avg_s": prof["combine_ms"] / calls * 1e-3}
     t_fused = timed(torch, step_fused, steps, warmup)
     prof_f = profiled(torch, st, step_fused, steps)
     fused_attn_avg = prof_f["attn_ms"] / prof_f["calls"] * 1e-3
@@ -189,6 +203,10 @@ def bench_cfg3(torch, qkv, steps, warmup):
                 st.attend(l, 1, [0], [L], T, qs.data_ptr() + l * lt, os_.data_ptr() + l * lt)
 
         spec[f"T{T}_us_per_layer"] = timed(torch, spec_step, steps, warmup) / nl * 1e6
+        if T == 8:  # the other verify form on this packed store: one pass of the 8-wave kernel (k_verify)
+            st.config("wide", 1)
+            spec["T8_one_pass_us_per_layer"] = timed(torch, spec_step, steps, warmup) / nl * 1e6
+            st.config("wide", 2)
     ok = bool(torch.isfinite(out).all().item())
     return {
         "L": L, "ws": ws, "ring_positions": L - ws, "layers": nl,
@@ -419,6 +437,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--configs", default="1,2,3,4,5,6")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--step-only", action="store_true",
+                    help="config 3: only the headline step's one-layer calls (eager, event-timed, graph), for profiling")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run 5 plain device copies of MIB MiB (the byte-counter calibration for rocprofv3 --pmc)")
@@ -442,7 +462,7 @@ def main():
     cfgs = {int(c) for c in args.configs.split(",") if c}
     extra = {}
     if 3 in cfgs:
-        extra["cfg3"] = bench_cfg3(torch, qkv, args.steps, args.warmup)
+        extra["cfg3"] = bench_cfg3(torch, qkv, args.steps, args.warmup, args.step_only)
     if 1 in cfgs:
         extra["cfg1"] = bench_cfg1(torch, qkv, args.steps, args.warmup)
     if 2 in cfgs:
@@ -463,7 +483,16 @@ def main():
         roof = {"bound": "hbm", "achieved": ach / 1e9, "peak": HBM_PEAK / 1e9, "unit": "GB/s", "frac": ach / HBM_PEAK,
                 "traffic": traffic_from_profiles("attn_cfg3_traffic.json"),
                 "kernel": "k_attn<1,5,6> (one layer, 4 kv heads, 101,600 positions)",
-                "algorithmic_bytes_per_launch": c3["attn_kernel_bytes"]}
+                "algorithmic_bytes_per_launch": c3["attn_kernel_bytes"],
+                "clock": "mean launch duration from the dispatch timestamps (HIP events recorded by hipExtLaunchKernelGGL "
+                         "at the kernel's own start and end, on its launch stream) over a profiled pass of the step's "
+                         "one-layer calls, without rocprofv3; profiles/attn_cfg3.md holds the rocprofv3 kernel trace of "
+                         "the same calls (bench.py --configs 3 --no-cpu --step-only)",
+                "duration_us": c3["attn_kernel_avg_s"] * 1e6}
+        tr = rocprof_duration("attn_cfg3_duration.json")
+        if tr:
+            roof["rocprof_mean_us"] = tr
+            roof["frac_rocprof"] = c3["attn_kernel_bytes"] / (tr * 1e-6) / HBM_PEAK
     line = {
         "metric": METRIC,
         "value": c3["positions_per_s"] if c3 else None,
@@ -475,6 +504,10 @@ def main():
         "config": {"workload": "cfg3: preset F (K5r/V6, win 2048) decode attention, L=101,600, 16 layers, T=1",
                    "layers": 16, "context": 101600, "kv_heads": 4, "q_heads": 24, "head_dim": 256,
                    "parallelism": "single GPU"},
+        "step_note": "one decode step = the 16 one-layer mk_kv_attend calls at L = 101,600, captured once as a HIP graph "
+                     "and replayed (every attention and combine kernel runs; the context length is the one fixed at "
+                     "capture, so a decoder whose L grows recaptures or updates the kernel nodes); the same calls issued "
+                     "eagerly from Python: extra.cfg3.eager_step_s",
         "gbps": c3["gbps"] if c3 else None,
         "hbm_frac": c3["gbps"] * 1e9 / HBM_PEAK if c3 else None,
         "append_us_per_step": extra.get("cfg2_append", {}).get("us_per_step"),

@@ -120,6 +120,11 @@ int mk_kv_attend_gated(void * h, int layer0, int n_layers, int n_seq, const int 
  * table.  The table is [rows][32] float2 (cos, sin) in device memory: the caller's (e.g. the reference's rewritten
  * image rows, engine.cu:30-62) via mk_kv_set_rope(h, table, rows), or with table = NULL the text table the reference
  * builds (loader.cu:1252-1258: p * 1e7^(-2i/64) in double, rounded to float), ctx rows, built once by the store.
+ * Exactness: the prep's arithmetic order is this library's own (FMA-chain partial sums, a 64-lane butterfly, 1/sqrtf);
+ * the reference's uses rsqrtf and a 32-lane reduction.  Prepped values therefore differ from the reference's by a few
+ * ulp, so K rows stored through mk_kv_append_prep / mk_kv_prefill_prep are bit-exact only against a restatement of
+ * this order (oracle kvo_qk_prep), not against the reference's stored bytes; the rows of mk_kv_append (already prepped
+ * input) are bit-exact against the reference's quantizers.
  */
 int mk_kv_set_rope(void * h, const void * table, int rows);
 

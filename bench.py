@@ -308,11 +308,17 @@ def bench_cfg4(torch, qkv, steps, warmup):
     gen_fill(torch, st, 0, L, nl, seed=3, outliers=False)
     q = torch.randn(nl, 1, T, NH, HD, device="cuda")
     out = torch.empty_like(q)
-    t = timed(torch, lambda: st.attend(0, nl, [0], [L], T, q.data_ptr(), out.data_ptr()), steps, warmup)
+    fn = lambda: st.attend(0, nl, [0], [L], T, q.data_ptr(), out.data_ptr())
+    t = timed(torch, fn, steps, warmup)
+    forms = {}
+    for name, wide in (("k_verify", 1), ("two_batches", 0)):  # both verify forms, the same bits
+        st.config("wide", wide)
+        forms[name + "_us_per_layer"] = timed(torch, fn, steps, warmup) / nl * 1e6
+    st.config("wide", 2)
     b = nl * NKV * L * 2 * BYTES[8]
     flops = nl * 2 * 2 * 48 * L * HD * NKV
     return {"L": L, "T": T, "layers": nl, "step_s": t, "us_per_layer": t / nl * 1e6, "gbps": b / t / 1e9,
-            "tflops": flops / t / 1e12, "positions_per_s": nl * L / t}
+            "tflops": flops / t / 1e12, "positions_per_s": nl * L / t, "forms": forms}
 
 
 def bench_cfg5(torch, qkv, steps, warmup):

@@ -830,7 +830,24 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SMALL ? 3 :
     for (int bitem = blockIdx.x; bitem < n_items; bitem += gridDim.x) {
         asm volatile("" : "+v"(lane));
         int n = lane & 15, q = lane >> 4;
-        const int nb = n_items / n_base, item = bitem / nb, batch = bitem - item * nb, row0 = RP * batch;
+        const int nb = n_items / n_base;
+        int item = bitem / nb, batch = bitem - item * nb;
+        if (nb == 2) {
+            // two row batches of one item run on workgroup indices 8 apart: the same XCD (workgroups are dealt to the
+            // 8 XCDs round robin by index) and dispatched together there, so the second batch's tile copies find the
+            // first's in that XCD's L2 instead of streaming the segment from HBM again.  The items past the last
+            // whole group of 8 keep the batch-minor order.
+            const int full = (n_base >> 3) << 3;
+            if (bitem < 2 * full) {
+                const int k = bitem >> 3;
+                item = ((k >> 1) << 3) + (bitem & 7);
+                batch = k & 1;
+            } else {
+                item = full + ((bitem - 2 * full) >> 1);
+                batch = (bitem - 2 * full) & 1;
+            }
+        }
+        const int row0 = RP * batch;
         int si = 0;
         SeqDesc sd = sd0;
         if (nseq > 1) {

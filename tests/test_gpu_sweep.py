@@ -1,7 +1,8 @@
 """A seeded randomized sweep over the store and attention parameters: per case a random MK_KV spec (bits 4..8 per side,
 rotations), window, context length, T (capped to one 640-bucket as the reference's att_cap_T does), 1..3 sequences
 on a shared page pool with a shuffled page table, and the decode occupancy knob.  Every stored row is compared bit for bit and every attention
-output within 2e-3 (max-abs relative) against the oracle.  QKV_SWEEP_CASES sets the number of cases (default 8)."""
+output within 2e-3 (max-abs relative) against the oracle.  QKV_SWEEP_CASES sets the number of cases (default 8);
+QKV_SWEEP_LONG_CASES the number of long-context cases (default 4)."""
 import os
 
 import numpy as np
@@ -49,6 +50,56 @@ def test_random_case(qkv, oracle, torch_gpu, case):
         st.append(s, 0, 1, 0, L, k.data_ptr(), v.data_ptr(), 0)
         torch.cuda.synchronize()
         check_rows(oracle, st, K, V, seq=s, ring_from=max(0, L - qkv.ring_rows(win)) if win else 0)
+        data.append((K, V))
+    Q = rng.standard_normal((1, n_seq, T, NH, HD)).astype(np.float32)
+    q = torch.from_numpy(Q).cuda()
+    o = torch.full_like(q, float("nan"))
+    st.attend(0, 1, list(range(n_seq)), lens, T, q.data_ptr(), o.data_ptr())
+    torch.cuda.synchronize()
+    out = o.cpu().numpy()
+    kb, vb, kr, vr = st.kbits[0], st.vbits[0], st.krot[0], st.vrot[0]
+    for s, L in enumerate(lens):
+        K, V = data[s]
+        ws = qkv.window_start(L, win)
+        ref = expected_attention(oracle, Q[0, s], K[:, 0], V[:, 0], T, kr, vr, kb, vb, ws, win > 0 and kb != 8, win > 0 and vb != 8)
+        assert rel_err(out[0, s], ref) <= 2e-3, (case, spec, win, L, T)
+    st.close()
+
+
+@pytest.mark.parametrize("case", range(int(os.environ.get("QKV_SWEEP_LONG_CASES", "4"))))
+def test_random_long_case(qkv, oracle, torch_gpu, case):
+    """The same sweep at long contexts (16,385 .. 70,000 positions: several tiles per wave, the window start inside a
+    segment), 1..2 paged sequences, and the verify form knob at T >= 5 (the forms give the same bits, so any may run)."""
+    torch = torch_gpu
+    rng = np.random.default_rng(7000 + case)
+    spec = random_spec(rng)
+    win = int(rng.choice([0, 640, 2048]))
+    n_seq = int(rng.integers(1, 3))
+    page = 256
+    lens = [int(rng.integers(16385, 70001)) for _ in range(n_seq)]
+    ctx = max(lens) + page
+    npg = -(-ctx // page)
+    T = int(rng.integers(1, 9))
+    T = min([qkv.cap_T(L - T, T) for L in lens] + [T])
+    T = max(T, 1)
+    st = qkv.KVStore(spec, win=win, n_layers=1, n_seq=n_seq, ctx=ctx, page=page, n_pages=n_seq * npg)
+    occ = int(rng.choice([0, 2, 3]))
+    wide = int(rng.choice([0, 1, 2]))
+    st.config("occupancy", occ)
+    st.config("wide", wide)
+    perm = rng.permutation(n_seq * npg)
+    data = []
+    print(f"long case {case}: spec={spec} win={win} lens={lens} T={T} occupancy={occ} wide={wide}", flush=True)
+    for s, L in enumerate(lens):
+        st.set_pages(s, perm[s * npg:(s + 1) * npg])
+        K, V = synth_kv(rng, L, 1, outliers=bool(rng.random() < 0.5))
+        K = K.astype(np.float16).astype(np.float32)
+        V = V.astype(np.float16).astype(np.float32)
+        for p in range(0, L, 16384):
+            k = torch.from_numpy(K[p:p + 16384]).half().cuda()
+            v = torch.from_numpy(V[p:p + 16384]).half().cuda()
+            st.append(s, 0, 1, p, k.shape[0], k.data_ptr(), v.data_ptr(), 1)
+        torch.cuda.synchronize()
         data.append((K, V))
     Q = rng.standard_normal((1, n_seq, T, NH, HD)).astype(np.float32)
     q = torch.from_numpy(Q).cuda()

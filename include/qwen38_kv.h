@@ -9,9 +9,10 @@
  * `stream` is a hipStream_t (NULL: the default stream).  One handle is not thread-safe: calls on it are serialised by
  * the caller, as with the reference's engine.  The attend and prefill calls of one handle share its split-K workspace:
  * issue them on one stream (or order the streams between calls), or their partials overwrite each other.  The
- * workspace grows on demand; a buffer it outgrows is kept, not freed, until mk_free, so a HIP graph captured over an
- * earlier call stays valid after a larger call (its replays keep using the old, smaller buffer; a graph replay and an
- * eager call of one handle must still not overlap).
+ * workspace grows on demand (by at least 1.5 times); a buffer it outgrows is kept, not freed, until mk_free, so a HIP
+ * graph captured over an earlier call stays valid after a larger call (its replays keep using the old, smaller
+ * buffer; a graph replay and an eager call of one handle must still not overlap).  The kept buffers together stay
+ * below twice the live workspace.
  *
  * Shapes: NKV = 4 kv heads, NH = 24 query heads (GQA 6), head dim 256, up to 17 attention slots (layers), up to 8
  * query tokens per attend call, up to 8 sequences per attend call.

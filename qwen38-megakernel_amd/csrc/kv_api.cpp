@@ -180,9 +180,12 @@ struct Store {
     // Workspace buffers a larger call has replaced.  They stay allocated until the store is freed: work already
     // enqueued, and any HIP graph captured over an earlier call, still hold their addresses (a graph replays the raw
     // kernel arguments), so freeing them here would let a later replay read and write freed device memory.
+    // A buffer that has to grow takes at least 1.5 times its old size, so a context that grows step by step
+    // reallocates a logarithmic number of times and the retired buffers together stay below twice the live one.
     std::vector<void *> retired;
     void grow(void *& p, size_t & have, size_t need) {
         if (need <= have) return;
+        if (have) need = std::max(need, have + have / 2);
         void * q = nullptr;
         HCK(hipMalloc(&q, need));
         if (p) retired.push_back(p);

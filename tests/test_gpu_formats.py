@@ -9,7 +9,8 @@ store's last T positions):
   T = 1 through the one-group kernel at two and at three workgroups per CU (the small-stage kernel where the format
         has one; the two must be equal bitwise);
   T = 2 and 3 through the 16- and 24-row kernels;
-  T = 8 through the default verify form and through the other one (k_verify / two 24-row batches), bitwise equal.
+  T = 8 through the default verify form and through the other one (k_verify / two 24-row batches), bitwise equal,
+        and tokens 0 and 5 bitwise equal to one-token calls at their own lengths.
 One case at 200,031 positions (bucket 200,320, 13 tiles per wave) runs D at T = 1 and 8.
 """
 from concurrent.futures import ThreadPoolExecutor
@@ -103,6 +104,10 @@ def test_format_long_context(qkv, oracle, torch_gpu, name, spec, win):
                 st.config("wide", wide)
                 assert np.array_equal(_attend(torch, st, Q, L, T), out), (name, "wide", wide)
             st.config("wide", 2)
+            # T-invariance (bench/dattn_bench.cu:1140-1160): token t equals a one-token call at its own length
+            for t in (0, 5):
+                o1 = _attend(torch, st, Q[t:t + 1], L - T + t + 1, 1)
+                assert np.array_equal(o1[0], out[t]), (name, "token", t)
 
 
 def test_format_d_200031(qkv, oracle, torch_gpu):

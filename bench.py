@@ -69,6 +69,25 @@ def timed(torch, fn, steps, warmup):
     return (time.perf_counter() - t0) / steps
 
 
+def graph_call_us(torch, fn, n, reps=5):
+    """fn(stream) -- n library calls on that stream -- captured once as a HIP graph and replayed `reps` times:
+    wall-clock µs per call (every kernel of every call runs; the graph removes the host's per-call cost)."""
+    side = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        fn(side.cuda_stream)  # warm on the capture stream
+        side.synchronize()
+        with torch.cuda.graph(graph, stream=side):
+            fn(torch.cuda.current_stream().cuda_stream)
+    graph.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        graph.replay()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / (reps * n) * 1e6
+
+
 def profiled(torch, st, fn, steps):
     """`steps` calls of fn with the store's kernel timing on (after one untimed call); the event totals + wall time."""
     fn()
@@ -238,11 +257,17 @@ def bench_cfg1(torch, qkv, steps, warmup):
     prof = profiled(torch, st, fn, steps * 5)
     attn = prof["attn_ms"] / prof["calls"] * 1e-3
     comb = prof["combine_ms"] / prof["calls"] * 1e-3
+    ncalls = 64
+    tg = graph_call_us(torch, lambda stream: [st.attend(0, 1, [0], [L], 1, q.data_ptr(), out.data_ptr(), stream=stream)
+                                              for _ in range(ncalls)], ncalls) * 1e-6
     b = NKV * L * 2 * BYTES[8]
     return {"L": L, "call_s": t, "positions_per_s": L / t, "gbps": b / t / 1e9,
+            "graph_call_s": tg, "graph_positions_per_s": L / tg,
             "attn_kernel_avg_s": attn, "combine_avg_s": comb, "attn_kernel_gbps": b / attn / 1e9,
-            "note": "8.9 MB per call: resident in the 256 MB last-level cache across calls; the kernel times come from "
-                    "a second pass with per-launch events, which lengthen short launches"}
+            "note": "call_s: one library call at a time from Python (the host's per-call cost included); graph_call_s: 64 "
+                    "calls captured once as a HIP graph and replayed (the GPU's time per call, as a serving loop issues "
+                    "them). 8.9 MB per call: resident in the 256 MB last-level cache across calls; the kernel times "
+                    "come from a second pass with per-launch events, which lengthen short launches"}
 
 
 def bench_cfg2(torch, qkv, nsteps=512):
@@ -272,24 +297,7 @@ def bench_cfg2(torch, qkv, nsteps=512):
     t = (time.perf_counter() - t0) / nsteps
     prof = profiled(torch, st, run, 1)
 
-    def graph_us(fn):
-        """fn(stream) captured once as a HIP graph, replayed 5 times: wall-clock µs per step."""
-        side = torch.cuda.Stream()
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.stream(side):
-            fn(side.cuda_stream)  # warm on the capture stream
-            side.synchronize()
-            with torch.cuda.graph(graph, stream=side):
-                fn(torch.cuda.current_stream().cuda_stream)
-        graph.replay()
-        torch.cuda.synchronize()
-        reps = 5
-        t0 = time.perf_counter()
-        for _ in range(reps):
-            graph.replay()
-        torch.cuda.synchronize()
-        return (time.perf_counter() - t0) / (reps * nsteps) * 1e6
-
+    graph_us = lambda fn: graph_call_us(torch, fn, nsteps)
     tg = graph_us(run) * 1e-6
     # the dispatch floor of one graph node (a one-element add), and the steps with cache-resident input rows
     one = torch.zeros(1, device="cuda")

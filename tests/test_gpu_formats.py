@@ -11,14 +11,15 @@ store's last T positions):
   T = 2 and 3 through the 16- and 24-row kernels;
   T = 8 through the default verify form and through the other one (k_verify / two 24-row batches), bitwise equal,
         and tokens 0 and 5 bitwise equal to one-token calls at their own lengths.
-One case at 200,031 positions (bucket 200,320, 13 tiles per wave) runs D at T = 1 and 8.
+One case at 200,031 positions (bucket 200,320, 13 tiles per wave) runs D at T = 1 and 8.  The prefill kernel of each
+format (k_prefill3, one instantiation per (K bits, V bits) pair as well) runs a 2,600-position prompt.
 """
 from concurrent.futures import ThreadPoolExecutor
 
 import numpy as np
 import pytest
 
-from kvcase import GQA, HD, NH, NKV, append_all, expected_kv, rel_err, synth_kv
+from kvcase import GQA, HD, NH, NKV, append_all, expected_attention, expected_kv, rel_err, synth_kv
 
 pytestmark = pytest.mark.gpu
 TOL = 2e-3
@@ -127,3 +128,29 @@ def test_format_d_200031(qkv, oracle, torch_gpu):
             st.config("occupancy", 3)
             assert np.array_equal(_attend(torch, st, Q, L, T), out)
             st.config("occupancy", 0)
+
+
+@pytest.mark.parametrize("name,spec,win", FORMATS, ids=[f[0] for f in FORMATS])
+def test_format_prefill(qkv, oracle, torch_gpu, name, spec, win):
+    """The prefill kernel of each format (its own (K bits, V bits) instantiation): a 2,600-position prompt in two chunks
+    over five 640-position pieces (packed rows below the window start, ring rows from it), the first and the last piece
+    against the oracle within 2e-3, and the same prompt in one chunk bitwise equal."""
+    from test_gpu_prefill import pieces, run_prefill
+
+    torch = torch_gpu
+    rng = np.random.default_rng(900 + len(name) * 3 + win % 11)
+    P = 2600
+    K, V = synth_kv(rng, P, 1, outliers=True)
+    Q = rng.standard_normal((1, P, NH, HD)).astype(np.float32)
+    st, out = run_prefill(qkv, torch, spec, win, K, V, Q, [1300, 1300], P)
+    kb, vb, kr, vr = st.kbits[0], st.vbits[0], st.krot[0], st.vrot[0]
+    for a, b in (pieces(P)[0], pieces(P)[-1]):
+        ws = qkv.window_start(b, win)
+        ref = expected_attention(oracle, Q[0, a:b], K[:b, 0], V[:b, 0], b - a, kr, vr, kb, vb, ws, win > 0 and kb != 8,
+                                 win > 0 and vb != 8)
+        e = rel_err(out[0, a:b], ref)
+        assert e <= TOL, (name, a, b, e)
+    st.close()
+    st2, out2 = run_prefill(qkv, torch, spec, win, K, V, Q, [P], P)
+    assert np.array_equal(out2, out), name
+    st2.close()

@@ -542,6 +542,7 @@ static int attend_impl(void * h, int layer0, int n_layers, int n_seq, const int 
             d.ws = window_start(L, s.win);
             d.cs = seg_len(L);
             d.nseg = (L + d.cs - 1) / d.cs;
+            d.nseg_m = magic31(d.nseg);
             seg_total += d.nseg;
             // pages pbase, pbase + 1, .. for every logical page the context touches: no table lookups in the kernel
             const int * pt = s.ptab.data() + (size_t) d.seq * s.pt_stride;
@@ -621,6 +622,7 @@ static int attend_impl(void * h, int layer0, int n_layers, int n_seq, const int 
                 b.ml = ml_base + item_base * a.R;
             }
             item_base += (size_t) item;
+            fill_head(b);
             groups[ng++] = b;
             l = e;
         }

@@ -38,14 +38,17 @@ constexpr unsigned C64 = 0x64646464u;
 // of a tile's, so the tile loops look a tile's page up one step ahead (page_of), before they wait for the current tile.
 typedef const __attribute__((address_space(4))) int * const_int_p;
 
-// physical page of the logical page holding position p (wave-uniform) of sequence seq
-__device__ __forceinline__ int page_of(const StoreLayout & S, int seq, int p) {
+// physical page of the logical page holding position p (wave-uniform) of sequence seq; Geo: StoreLayout or RowGeo (the
+// same member names)
+template <class Geo>
+__device__ __forceinline__ int page_of(const Geo & S, int seq, int p) {
     const int lp = __builtin_amdgcn_readfirstlane(p / S.page);
     return ((const_int_p) S.ptab)[seq * S.pt_stride + lp];
 }
 
 // main-store row of (g, p) in physical page phys (the page of p)
-__device__ __forceinline__ size_t attn_main_row(const StoreLayout & S, int g, int p, int phys) {
+template <class Geo>
+__device__ __forceinline__ size_t attn_main_row(const Geo & S, int g, int p, int phys) {
     const int lp = __builtin_amdgcn_readfirstlane(p / S.page);
     return (size_t) (g * S.n_pages + phys) * S.page + (p - lp * S.page);
 }
@@ -294,15 +297,13 @@ struct TileSrc {
 
 // the source rows of the 32 positions from p0 (wave-uniform) of (seq, kv head g): window tiles (ring) are q8 rows
 // from the ring of sides that have one, else from the main store (q8 sides); other tiles are main-store rows of
-// KB / VB bits.  ring0 = the first ring row of (seq, g).
-// phys: the physical page of p0 (page_of), looked up by the caller
+// KB / VB bits.  ring0 = the first ring row of (seq, g); mr = the main-store row of p0 (read only for a side without a
+// ring or a packed tile)
 template <int KB, int VB>
-__device__ __forceinline__ TileSrc tile_src(const StoreLayout & S, const SideLayout & SK, const SideLayout & SV, int g, int p0, int phys,
-                                           size_t ring0, bool ring) {
+__device__ __forceinline__ TileSrc tile_src_row(int kvrc, const SideLayout & SK, const SideLayout & SV, size_t mr, int p0, size_t ring0,
+                                               bool ring) {
     TileSrc t;
-    size_t mr = 0;
-    if (!ring || !SK.ring || !SV.ring) mr = attn_main_row(S, g, p0, phys);
-    const size_t rr = ring ? ring0 + __builtin_amdgcn_readfirstlane(p0 % max(S.kvrc, 1)) : 0;
+    const size_t rr = ring ? ring0 + __builtin_amdgcn_readfirstlane(p0 % max(kvrc, 1)) : 0;
     if (ring && SK.ring) {
         t.k = reinterpret_cast<const uint8_t *>(SK.ring) + rr * HD;
         t.ks = SK.rsc + rr * 8;
@@ -318,6 +319,13 @@ __device__ __forceinline__ TileSrc tile_src(const StoreLayout & S, const SideLay
         t.vs = SV.scs + mr * 8;
     }
     return t;
+}
+// the same with the main-store row from phys, the physical page of p0 (page_of), looked up by the caller
+template <int KB, int VB, class Geo>
+__device__ __forceinline__ TileSrc tile_src(const Geo & S, const SideLayout & SK, const SideLayout & SV, int g, int p0, int phys,
+                                           size_t ring0, bool ring) {
+    const size_t mr = !ring || !SK.ring || !SV.ring ? attn_main_row(S, g, p0, phys) : 0;
+    return tile_src_row<KB, VB>(S.kvrc, SK, SV, mr, p0, ring0, ring);
 }
 
 // copies of one tile into the stage at LDS address `lds` (KB + VB + 1 copy instructions per lane).
@@ -788,6 +796,42 @@ __device__ __forceinline__ void set_prio(int left) {
     else __builtin_amdgcn_s_setprio(0);
 }
 
+// ------------------------------------------------------------------------------------------------ launch head
+// AttnHead (the first 192 bytes of the kernel arguments) in scalar registers: three 16-dword loads and one wait.  The
+// values come out of the asm, so the compiler keeps them in registers (or VGPR lanes) and never re-reads a field from
+// the argument segment in the middle of the prologue.
+typedef unsigned u32x16 __attribute__((ext_vector_type(16)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+struct HeadRegs {
+    u32x16 a, b, c;
+    u32x4 d;
+};
+__device__ __forceinline__ HeadRegs load_head() {
+    HeadRegs r;
+    asm volatile("s_load_dwordx16 %0, %4, 0x0\n\ts_load_dwordx16 %1, %4, 0x40\n\ts_load_dwordx16 %2, %4, 0x80\n\t"
+                 "s_load_dwordx4 %3, %4, 0xc0\n\ts_waitcnt lgkmcnt(0)"
+                 : "=&s"(r.a), "=&s"(r.b), "=&s"(r.c), "=&s"(r.d)
+                 : "s"(__builtin_amdgcn_kernarg_segment_ptr()));
+    return r;
+}
+template <int I>
+__device__ __forceinline__ unsigned head_dw(const HeadRegs & r) {
+    if constexpr (I < 16) return r.a[I];
+    else if constexpr (I < 32) return r.b[I - 16];
+    else if constexpr (I < 48) return r.c[I - 32];
+    else return r.d[I - 48];
+}
+template <typename T, int OFF>
+__device__ __forceinline__ T head_get(const HeadRegs & r) {
+    static_assert(OFF % 4 == 0 && OFF + sizeof(T) <= sizeof(AttnHead), "a dword-aligned head field");
+    constexpr int I = OFF / 4;
+    if constexpr (sizeof(T) == 8) return __builtin_bit_cast(T, ((unsigned long long) head_dw<I + 1>(r) << 32) | head_dw<I>(r));
+    else return __builtin_bit_cast(T, head_dw<I>(r));
+}
+// floor(n / d) from M = magic31(d) (kv_launch.h): exact for n d < 2^31, one multiply instead of a division sequence
+__device__ __forceinline__ int div_m(int n, unsigned M) { return (int) __umulhi(2u * (unsigned) n, M); }
+#define QKV_HEAD(r, f) head_get<std::remove_cv_t<decltype(AttnHead::f)>, offsetof(AttnHead, f)>(r)
+
 // ------------------------------------------------------------------------------------------------ the kernel
 // More than 16 query rows (T >= 3) are held as 24 rows per wave (three groups; 48 rows of accumulators in one wave
 // spill).  T = 3, 4: one 24-row pass.  T = 5..8: k_verify below (one pass, 8 waves), or (knob) batches of 24 rows
@@ -812,27 +856,44 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SMALL ? 3 :
     // and the merge are not held (and spilled) across the tile loop, as a spill reload waits for every copy in flight
     int lane = threadIdx.x & 63;
     const int sl = wv; // the wave's slice of tiles: w, w + 4, ..
-    const StoreLayout & S = a.S;
+    const StoreLayout & S = a.S; // (the layouts of layers after layer0, the fused append's geometry)
     const unsigned lds0 = (unsigned) (size_t) (__attribute__((address_space(3))) uint8_t *) smem;
-    const unsigned st_lds = (unsigned) __builtin_amdgcn_readfirstlane(lds0 + wv * SB);
+    const unsigned st_lds0 = (unsigned) __builtin_amdgcn_readfirstlane(lds0 + wv * SB);
     half8 * const sQ = reinterpret_cast<half8 *>(smem + SLDS); // [RP][256] fp16, chunk-swizzled (qchunk)
     // The first tile copy of an item waits on every scalar load before it, and each round trip to the kernel arguments
-    // costs a few hundred ns at launch: the common case (one sequence, one layer) needs one round -- the header, sd[0]
-    // and side0 at fixed offsets, made live together by the empty asm so that the loads issue back to back and are
-    // waited for once -- and only other sequences / layers add a second.
-    const int n_items = a.n_items, n_base = a.n_base, nseq = a.nseq, kvrc = S.kvrc, spage = S.page;
-    const SeqDesc sd0 = a.sd[0];
-    const SideLayout K0 = a.side0[0], V0 = a.side0[1];
-    asm volatile("" ::"s"(n_items), "s"(n_base), "s"(nseq), "s"(kvrc), "s"(spage), "s"(sd0.L), "s"(sd0.ws), "s"(sd0.cs), "s"(sd0.nseg),
-                 "s"(sd0.item0), "s"(sd0.pbase), "s"(sd0.seq), "s"(K0.vals), "s"(K0.scs), "s"(K0.ring), "s"(K0.rsc), "s"(V0.vals),
-                 "s"(V0.scs), "s"(V0.ring), "s"(V0.rsc), "s"(a.T), "s"(a.R), "s"(a.layer0), "s"(a.krot), "s"(a.qs), "s"(a.q),
-                 "s"(a.qnw), "s"(a.rope), "s"(S.ptab), "s"(S.pt_stride));
+    // costs a few hundred ns at launch: the common case (one sequence, one layer) takes everything from the launch head
+    // (AttnHead, one round of loads); only other sequences / layers read more.
+    const HeadRegs hr = load_head();
+    const int n_items = QKV_HEAD(hr, n_items), n_base = QKV_HEAD(hr, n_base), nseq0 = QKV_HEAD(hr, nseq), kvrc = QKV_HEAD(hr, kvrc),
+              spage = QKV_HEAD(hr, page);
+    const int T = QKV_HEAD(hr, T), R = QKV_HEAD(hr, R), layer0 = QKV_HEAD(hr, layer0), qs = QKV_HEAD(hr, qs);
+    const unsigned krot = QKV_HEAD(hr, krot);
+    const int * const ptab = QKV_HEAD(hr, ptab);
+    const int pt_stride = QKV_HEAD(hr, pt_stride), n_pages = QKV_HEAD(hr, n_pages);
+    const SeqDesc sd0{QKV_HEAD(hr, seq),  QKV_HEAD(hr, L),     QKV_HEAD(hr, ws),   QKV_HEAD(hr, cs),
+                      QKV_HEAD(hr, nseg), QKV_HEAD(hr, item0), QKV_HEAD(hr, pbase), QKV_HEAD(hr, nseg_m)};
+    const unsigned T_m = QKV_HEAD(hr, T_m);
+    const SideLayout K0{QKV_HEAD(hr, kvals), QKV_HEAD(hr, kscs), QKV_HEAD(hr, kring), QKV_HEAD(hr, krsc), APPEND ? a.side0[0].bits : KB,
+                        APPEND ? a.side0[0].rot : 0};
+    const SideLayout V0{QKV_HEAD(hr, vvals), QKV_HEAD(hr, vscs), QKV_HEAD(hr, vring), QKV_HEAD(hr, vrsc), APPEND ? a.side0[1].bits : VB,
+                        APPEND ? a.side0[1].rot : 0};
+    const float * const qp = QKV_HEAD(hr, q);
+    const float * const qnw = QKV_HEAD(hr, qnw);
+    const float2 * const rope = QKV_HEAD(hr, rope);
+    float * const part = QKV_HEAD(hr, part);
+    float2 * const ml = QKV_HEAD(hr, ml);
     for (int bitem = blockIdx.x; bitem < n_items; bitem += gridDim.x) {
         asm volatile("" : "+v"(lane));
+        // the stage address and the sequence count are made opaque per item as well: values derived from them (the 16
+        // copy destinations of a stage, the sequence tests) are computed where they are used instead of once before
+        // the loop and kept in VGPR lanes, which costs more instructions before an item's first copy than it saves
+        unsigned st_lds = st_lds0;
+        int nseq = nseq0;
+        asm volatile("" : "+s"(st_lds), "+s"(nseq));
         int n = lane & 15, q = lane >> 4;
-        const int nb = n_items / n_base;
-        int item = bitem / nb, batch = bitem - item * nb;
-        if (nb == 2) {
+        // one row batch per item, or two (n_items = 2 n_base: T = 5..8 in 24-row batches)
+        int item = bitem, batch = 0;
+        if (n_items != n_base) {
             // two row batches of one item run on workgroup indices 8 apart: the same XCD (workgroups are dealt to the
             // 8 XCDs round robin by index) and dispatched together there, so the second batch's tile copies find the
             // first's in that XCD's L2 instead of streaming the segment from HBM again.  The items past the last
@@ -860,24 +921,27 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SMALL ? 3 :
             sd = a.sd[si];
         }
         const int local = item - sd.item0;
-        const int seg = local % sd.nseg, lg = local / sd.nseg;
+        const int lg = div_m(local, sd.nseg_m), seg = local - lg * sd.nseg;
         const int g = lg % NKV, l = lg / NKV;
-        const int L = sd.L, ws = sd.ws, seq = sd.seq, T = a.T;
+        const int L = sd.L, ws = sd.ws, seq = sd.seq;
         const int c0 = seg * sd.cs, c1 = min(L, c0 + sd.cs);
         const int ntiles = (c1 - c0 + ATP - 1) / ATP;
         const int my = ntiles > sl ? (ntiles - sl + AWAVES - 1) / AWAVES : 0; // tiles sl, sl+4, ..
         SideLayout SK = K0, SV = V0;
         if (l > 0) {
-            SK = S.side[a.layer0 + l][0];
-            SV = S.side[a.layer0 + l][1];
+            SK = S.side[layer0 + l][0];
+            SV = S.side[layer0 + l][1];
         }
+        const RowGeo geo{ptab, pt_stride, spage, n_pages, kvrc};
         const size_t ring0 = (size_t) (seq * NKV + g) * kvrc;
+        const size_t gbase = (size_t) (g * n_pages + sd.pbase) * spage;
+        auto main_row_of = [&](int p, int phys) { return sd.pbase >= 0 ? gbase + p : attn_main_row(geo, g, p, phys); };
 
         // tile i of the wave starts at position c0 + 32 (sl + 4 i); phys: its physical page; into the stage at lds_to
         auto issue = [&](int i, int phys, unsigned lds_to) {
             const int p0 = c0 + ATP * (sl + AWAVES * i), nv = min(ATP, L - p0);
-            const bool ring = S.kvrc > 0 && p0 >= ws; // the window: q8 rows (ring, or the main store of q8 sides)
-            const TileSrc t = tile_src<KB, VB>(S, SK, SV, g, p0, phys, ring0, ring);
+            const bool ring = kvrc > 0 && p0 >= ws; // the window: q8 rows (ring, or the main store of q8 sides)
+            const TileSrc t = tile_src_row<KB, VB>(kvrc, SK, SV, main_row_of(p0, phys), p0, ring0, ring);
             int ln = lane; // opaque: the per-lane chunk addresses are not hoisted out of the tile loop into registers
             asm volatile("" : "+v"(ln));
             // 24-row kernels (NP = 3) run T = 5..8 as two row batches that stream the same tiles: no non-temporal hint
@@ -890,11 +954,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SMALL ? 3 :
             }
         };
 
-        // physical page of tile i: the table is read only for sequences whose pages are not contiguous
-        auto tile_page = [&](int i) {
-            const int p = c0 + ATP * (sl + AWAVES * i);
-            return sd.pbase >= 0 ? sd.pbase + __builtin_amdgcn_readfirstlane(p / spage) : page_of(S, seq, p);
-        };
+        // physical page of tile i: the table is read only for sequences whose pages are not contiguous (0 otherwise:
+        // the main-store row of position p is then gbase + p)
+        auto tile_page = [&](int i) { return sd.pbase >= 0 ? 0 : page_of(geo, seq, c0 + ATP * (sl + AWAVES * i)); };
         int phys_cur = my > 0 ? tile_page(0) : 0; // page of the tile in the stage (tile i while step i runs)
         // fused append (APPEND kernels only): a wave whose tiles hold new positions (L - T .. L - 1) stores those rows
         // before its first copy (a called function waits for every load at entry, so it runs before any copy is issued)
@@ -909,7 +971,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SMALL ? 3 :
         // the wait (the loaded registers must not be read or moved before it).
         if constexpr (APPEND)
             if (has_new) {
-                append_rows(a.kin, a.vin, a.kin_f16, a.kin_nl, S.ptab, S.pt_stride, S.page, S.n_pages, S.kvrc, SK.vals, SK.scs, SK.ring,
+                append_rows(a.kin, a.vin, a.kin_f16, a.kin_nl, geo.ptab, geo.pt_stride, geo.page, geo.n_pages, geo.kvrc, SK.vals, SK.scs, SK.ring,
                             SK.rsc, SK.bits, SK.rot, SV.vals, SV.scs, SV.ring, SV.rsc, SV.bits, SV.rot, seq, g, l, si, L, T, c0, c1, sl, 0, 1);
                 vm_wait<0>(); // the stored rows are in L2 before this wave's copies read them
             }
@@ -918,9 +980,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SMALL ? 3 :
 #pragma unroll
         for (int j = 0; j < QPW; j++) {
             const int r = row0 + wv + AWAVES * j;
-            if (r < a.R) {
-                const int hh = r / T, t = r % T;
-                qx[j] = gload16(a.q + (((size_t) (l * a.nseq + si) * T + t) * NH + GQA * g + hh) * a.qs + 4 * lane);
+            if (r < R) {
+                const int hh = div_m(r, T_m), t = r - hh * T;
+                qx[j] = gload16(qp + (((size_t) (l * nseq + si) * T + t) * NH + GQA * g + hh) * qs + 4 * lane);
             } else {
                 qx[j] = f32x4{0.f, 0.f, 0.f, 0.f};
             }
@@ -928,7 +990,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SMALL ? 3 :
         if (my > 0) {
             issue(0, phys_cur, st_lds);
             // copy instructions of tile 0 (issue_tile / issue_q8_part): every load before them has returned
-            const bool ring = S.kvrc > 0 && c0 + ATP * sl >= ws;
+            const bool ring = kvrc > 0 && c0 + ATP * sl >= ws;
             if (ring) {
                 vm_wait<SMALL ? 8 + 1 : 8 + 8 + 1>();
             } else {
@@ -942,11 +1004,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SMALL ? 3 :
             pin_after(qx[j]);
             const int r = wv + AWAVES * j, gr = row0 + r;
             half2v o0 = {(_Float16) 0.f, (_Float16) 0.f}, o1 = o0;
-            if (gr < a.R) {
-                const int t = gr % T;
+            if (gr < R) {
+                const int t = gr - div_m(gr, T_m) * T;
                 float v[4] = {qx[j][0], qx[j][1], qx[j][2], qx[j][3]};
-                if (a.qnw) qk_prep(v, a.qnw + (size_t) l * HD, a.rope + (size_t) (L - T + t) * 32);
-                if ((a.krot >> (a.layer0 + l)) & 1u) fwht256_w64(v);
+                if (qnw) qk_prep(v, qnw + (size_t) l * HD, rope + (size_t) (L - T + t) * 32);
+                if ((krot >> (layer0 + l)) & 1u) fwht256_w64(v);
                 o0[0] = (_Float16) (v[0] * 0.0625f);
                 o0[1] = (_Float16) (v[1] * 0.0625f);
                 o1[0] = (_Float16) (v[2] * 0.0625f);
@@ -963,7 +1025,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SMALL ? 3 :
                 st.m[H] = -INFINITY;
                 st.l[H] = 0.f;
                 const int row = row0 + 16 * H + n; // (block 1, lanes 8..15: padding)
-                st.lim[H] = (H == 0 || n < 8) && row < a.R ? L - T + row % T : -1;
+                st.lim[H] = (H == 0 || n < 8) && row < R ? L - T + (row - div_m(row, T_m) * T) : -1;
             }
         } else {
 #pragma unroll
@@ -971,7 +1033,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SMALL ? 3 :
                 st.m[h] = -INFINITY;
                 st.l[h] = 0.f;
                 const int row = row0 + 8 * h + (n >> 1);
-                st.lim[h] = row < a.R ? L - T + row % T : -1;
+                st.lim[h] = row < R ? L - T + (row - div_m(row, T_m) * T) : -1;
             }
         }
 #pragma unroll
@@ -998,7 +1060,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SMALL ? 3 :
                 read_k<8, 8>(raw, stp, sc, n, q);
                 lds_drain(); // the K rows are in registers: the V half may overwrite them
                 {
-                    const TileSrc t = tile_src<KB, VB>(S, SK, SV, g, p0, phys_cur, ring0, true);
+                    const TileSrc t = tile_src_row<KB, VB>(kvrc, SK, SV, main_row_of(p0, phys_cur), p0, ring0, true);
                     int ln = lane;
                     asm volatile("" : "+v"(ln));
                     issue_q8_part<1>(t, min(ATP, L - p0), st_lds, ln);
@@ -1044,7 +1106,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SMALL ? 3 :
         // the wave's window (ring) tiles are its last ones: i >= i_ring, p0 >= ws.  Two loops, one tile format each,
         // keep a single tile body live per loop (one body holding both formats costs registers)
         int i_ring = my;
-        if (S.kvrc > 0) {
+        if (kvrc > 0) {
             const int d = ws - c0 - ATP * sl;
             i_ring = d <= 0 ? 0 : min(my, (d + AWAVES * ATP - 1) / (AWAVES * ATP));
         }
@@ -1081,7 +1143,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SMALL ? 3 :
             }
         }
         __syncthreads();
-        const int R = a.R, RB = min(RP, R - row0); // rows of this batch
+        const int RB = min(RP, R - row0); // rows of this batch
         constexpr int NPASS = (NP + 1) / 2;
 #pragma unroll
         for (int ps = 0; ps < NPASS; ps++) {
@@ -1114,7 +1176,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SMALL ? 3 :
                     y.z += z.z;
                     y.w += z.w;
                 }
-                store_part(a.part + ((size_t) item * R + row0 + 16 * ps + r16) * HD + 4 * c4, y);
+                store_part(part + ((size_t) item * R + row0 + 16 * ps + r16) * HD + 4 * c4, y);
             }
             if (ps + 1 < NPASS) __syncthreads();
         }
@@ -1127,7 +1189,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SMALL ? 3 :
                 const float ew = s_m[w * RP + row] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(s_m[w * RP + row] - M);
                 lsum += ew * s_l[w * RP + row];
             }
-            a.ml[(size_t) item * R + row0 + row] = make_float2(M, lsum);
+            ml[(size_t) item * R + row0 + row] = make_float2(M, lsum);
         }
         __syncthreads(); // the LDS is reused by the next item
     }

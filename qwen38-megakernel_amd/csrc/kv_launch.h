@@ -15,9 +15,41 @@ struct SeqDesc {
     int nseg;  // segments: ceil(L / cs) <= 128
     int item0; // first work item of this sequence in the launch
     int pbase; // >= 0: the sequence's pages are pbase, pbase + 1, .. (no table lookup); -1: read the page table
+    unsigned nseg_m; // magic31(nseg)
 };
 
+// ceil(2^31 / d): floor(n / d) = (2 n * magic31(d)) >> 32 exactly for 0 <= n, 1 <= d with n d < 2^31 (div_m)
+inline unsigned magic31(int d) { return (unsigned) (((1ull << 31) + (unsigned) d - 1) / (unsigned) d); }
+
+// The scalars a decode workgroup (k_attn) needs before its first tile copy and for its merge, as 52 dwords at offset 0
+// of the kernel arguments: the kernel reads them with four scalar loads and one wait, into registers the
+// compiler cannot refill from memory later (it would otherwise re-read fields from the argument segment, each re-read
+// a round trip under the launch's load, several of them in series before the first copy).
+struct AttnHead {
+    uint8_t * kvals; // side0[0]: K of slot layer0
+    uint16_t * kscs;
+    int8_t * kring;
+    uint16_t * krsc;
+    uint8_t * vvals; // side0[1]: V of slot layer0
+    uint16_t * vscs;
+    int8_t * vring;
+    uint16_t * vrsc;
+    const float * q;       // AttnArgs::q, part, ml, S.ptab, qnw, rope
+    float * part;
+    float2 * ml;
+    const int * ptab;
+    const float * qnw;
+    const float2 * rope;
+    int L, ws, cs, nseg, item0, pbase, seq;                                       // sd[0]
+    int n_items, n_base, nseq, T, R, layer0, qs, kvrc, page, n_pages, pt_stride; // AttnArgs / S fields of the same names
+    unsigned krot;
+    unsigned nseg_m, T_m; // magic31(nseg of sd[0]), magic31(T)
+    int pad[3];
+};
+static_assert(sizeof(AttnHead) == 208, "three 16-dword loads and one 4-dword load");
+
 struct AttnArgs {
+    AttnHead h;          // (k_attn's copy of the fields below, filled by fill_head)
     // first: what a workgroup needs before its first tile copy, at fixed offsets (one round of scalar loads)
     SideLayout side0[2]; // K, V layouts of slot layer0 (S.side[layer0])
     StoreLayout S;
@@ -48,6 +80,48 @@ struct AttnArgs {
     const void * vin;
     int kin_nl, kin_f16;
 };
+
+// AttnHead from the launch's other fields (after they are final)
+inline void fill_head(AttnArgs & a) {
+    AttnHead & h = a.h;
+    h.kvals = a.side0[0].vals;
+    h.kscs = a.side0[0].scs;
+    h.kring = a.side0[0].ring;
+    h.krsc = a.side0[0].rsc;
+    h.vvals = a.side0[1].vals;
+    h.vscs = a.side0[1].scs;
+    h.vring = a.side0[1].ring;
+    h.vrsc = a.side0[1].rsc;
+    h.q = a.q;
+    h.part = a.part;
+    h.ml = a.ml;
+    h.ptab = a.S.ptab;
+    h.qnw = a.qnw;
+    h.rope = a.rope;
+    const SeqDesc & d = a.sd[0];
+    h.L = d.L;
+    h.ws = d.ws;
+    h.cs = d.cs;
+    h.nseg = d.nseg;
+    h.item0 = d.item0;
+    h.pbase = d.pbase;
+    h.seq = d.seq;
+    h.n_items = a.n_items;
+    h.n_base = a.n_base;
+    h.nseq = a.nseq;
+    h.T = a.T;
+    h.R = a.R;
+    h.layer0 = a.layer0;
+    h.qs = a.qs;
+    h.kvrc = a.S.kvrc;
+    h.page = a.S.page;
+    h.n_pages = a.S.n_pages;
+    h.pt_stride = a.S.pt_stride;
+    h.krot = a.krot;
+    h.nseg_m = d.nseg_m;
+    h.T_m = magic31(a.T);
+    h.pad[0] = h.pad[1] = h.pad[2] = 0;
+}
 
 // one prefill piece of one layer: query rows r = 6 t + hh (token t = 0 .. Tp-1 at position n0 + t, query head
 // 6 g + hh of kv head g), keys in absolute segments of `seg` positions (pf_seg of the piece's bucket)

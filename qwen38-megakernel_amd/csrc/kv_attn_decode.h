@@ -303,7 +303,12 @@ template <int KB, int VB>
 __device__ __forceinline__ TileSrc tile_src_row(int kvrc, const SideLayout & SK, const SideLayout & SV, size_t mr, int p0, size_t ring0,
                                                bool ring) {
     TileSrc t;
-    const size_t rr = ring ? ring0 + __builtin_amdgcn_readfirstlane(p0 % max(kvrc, 1)) : 0;
+    size_t rr = 0;
+    if (ring) {
+        int rows = max(kvrc, 1);
+        asm volatile("" : "+s"(rows)); // the division's set-up stays on this path (not hoisted out of a caller's loop)
+        rr = ring0 + __builtin_amdgcn_readfirstlane(p0 % rows);
+    }
     if (ring && SK.ring) {
         t.k = reinterpret_cast<const uint8_t *>(SK.ring) + rr * HD;
         t.ks = SK.rsc + rr * 8;
@@ -935,7 +940,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SMALL ? 3 :
         const RowGeo geo{ptab, pt_stride, spage, n_pages, kvrc};
         const size_t ring0 = (size_t) (seq * NKV + g) * kvrc;
         const size_t gbase = (size_t) (g * n_pages + sd.pbase) * spage;
-        auto main_row_of = [&](int p, int phys) { return sd.pbase >= 0 ? gbase + p : attn_main_row(geo, g, p, phys); };
+        // (the page-table path divides by the page size, made opaque there, so that the division's set-up is
+        // not hoisted out of the item loop onto the common path)
+        auto paged_geo = [&]() {
+            RowGeo G = geo;
+            asm volatile("" : "+s"(G.page));
+            return G;
+        };
+        auto main_row_of = [&](int p, int phys) { return sd.pbase >= 0 ? gbase + p : attn_main_row(paged_geo(), g, p, phys); };
 
         // tile i of the wave starts at position c0 + 32 (sl + 4 i); phys: its physical page; into the stage at lds_to
         auto issue = [&](int i, int phys, unsigned lds_to) {
@@ -956,7 +968,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SMALL ? 3 :
 
         // physical page of tile i: the table is read only for sequences whose pages are not contiguous (0 otherwise:
         // the main-store row of position p is then gbase + p)
-        auto tile_page = [&](int i) { return sd.pbase >= 0 ? 0 : page_of(geo, seq, c0 + ATP * (sl + AWAVES * i)); };
+        auto tile_page = [&](int i) { return sd.pbase >= 0 ? 0 : page_of(paged_geo(), seq, c0 + ATP * (sl + AWAVES * i)); };
         int phys_cur = my > 0 ? tile_page(0) : 0; // page of the tile in the stage (tile i while step i runs)
         // fused append (APPEND kernels only): a wave whose tiles hold new positions (L - T .. L - 1) stores those rows
         // before its first copy (a called function waits for every load at entry, so it runs before any copy is issued)

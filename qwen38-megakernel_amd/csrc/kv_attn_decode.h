@@ -1234,7 +1234,7 @@ __device__ __forceinline__ ItemGeo item_geo(const AttnArgs & a, int item) {
     for (int i = 1; i < MAX_SEQ; i++)
         if (i < a.nseq && item >= a.sd[i].item0) si = i;
     const SeqDesc sd = a.sd[si];
-    const int local = item - sd.item0, seg = local % sd.nseg, lg = local / sd.nseg;
+    const int local = item - sd.item0, lg = div_m(local, sd.nseg_m), seg = local - lg * sd.nseg;
     G.si = si;
     G.seq = sd.seq;
     G.L = sd.L;
@@ -1267,16 +1267,18 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     half8 * const sQ = reinterpret_cast<half8 *>(smem + NW * SB); // [48][256] fp16, chunk-swizzled per half of 24 rows
     const half8 * const sQh = sQ + hf * RP * (HD / 8);
     const int T = a.T, R = a.R;
+    const unsigned T_m = a.h.T_m;
 
-    auto tile_phys = [&](const ItemGeo & G, int p) {
-        return G.pbase >= 0 ? G.pbase + __builtin_amdgcn_readfirstlane(p / S.page) : page_of(S, G.seq, p);
-    };
+    // physical page of position p of item G: the table is read only for sequences whose pages are not contiguous (0
+    // otherwise: the main-store row of p is then (g n_pages + pbase) page + p)
+    auto tile_phys = [&](const ItemGeo & G, int p) { return G.pbase >= 0 ? 0 : page_of(S, G.seq, p); };
     // the wave's half of tile i of an item (its first position c0, length L, window start ws, kv head g, sides SK / SV,
     // first ring row ring0) into stage b
-    auto issue = [&](SideLayout SK, SideLayout SV, int c0, int L, int ws, int g, size_t ring0, int i, int phys, int b) {
+    auto issue = [&](SideLayout SK, SideLayout SV, int c0, int L, int ws, int g, int pbase, size_t ring0, int i, int phys, int b) {
         const int p0 = c0 + ATP * (sl + AWAVES * i), nv = min(ATP, L - p0);
         const bool ring = S.kvrc > 0 && p0 >= ws;
-        TileSrc t = tile_src<KB, VB>(S, SK, SV, g, p0, phys, ring0, ring);
+        const size_t mr = pbase >= 0 ? (size_t) (g * S.n_pages + pbase) * S.page + p0 : attn_main_row(S, g, p0, phys);
+        TileSrc t = tile_src_row<KB, VB>(S.kvrc, SK, SV, mr, p0, ring0, ring);
         t.k = uniform_ptr(t.k); // (wave-uniform by construction; stated, so that the copies take the scalar base)
         t.v = uniform_ptr(t.v);
         const unsigned to = (unsigned) __builtin_amdgcn_readfirstlane(lds0 + stage(b) * SB);
@@ -1292,7 +1294,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     };
     // the wave's query rows r = wv + 8 j of item G (rows hh T + t of the kv head)
     auto q_addr = [&](const ItemGeo & G, int j) {
-        const int r = wv + NW * j, hh = r / T, t = r % T;
+        const int r = wv + NW * j, hh = div_m(r, T_m), t = r - hh * T;
         return a.q + (((size_t) (G.l * a.nseq + G.si) * T + t) * NH + GQA * G.g + hh) * a.qs + 4 * lane;
     };
 
@@ -1328,7 +1330,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
             for (int j = 0; j < QPW; j++) qx[j] = wv + NW * j < R ? gload16(q_addr(G, j)) : f32x4{0.f, 0.f, 0.f, 0.f};
             if (my > 0) {
-                issue(SK, SV, G.c0, G.L, G.ws, G.g, G.ring0, 0, tile_phys(G, G.c0 + ATP * sl), par);
+                issue(SK, SV, G.c0, G.L, G.ws, G.g, G.pbase, G.ring0, 0, tile_phys(G, G.c0 + ATP * sl), par);
                 const bool ring = S.kvrc > 0 && G.c0 + ATP * sl >= G.ws;
                 if (ring) vm_wait<8 + 1>();
                 else if (hf == 0) vm_wait<KB + 1>();
@@ -1345,7 +1347,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             const int r = wv + NW * j;
             half2v o0 = {(_Float16) 0.f, (_Float16) 0.f}, o1 = o0;
             if (r < R) {
-                const int t = r % T;
+                const int t = r - div_m(r, T_m) * T;
                 float v[4] = {qx[j][0], qx[j][1], qx[j][2], qx[j][3]};
                 if (a.qnw) qk_prep(v, a.qnw + (size_t) G.l * HD, a.rope + (size_t) (G.L - T + t) * 32);
                 if ((a.krot >> (a.layer0 + G.l)) & 1u) fwht256_w64(v);
@@ -1362,7 +1364,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             st.m[H] = -INFINITY;
             st.l[H] = 0.f;
             const int row = row0 + 16 * H + n; // (block 1, lanes 8..15: padding)
-            st.lim[H] = (H == 0 || n < 8) && row < R ? G.L - T + row % T : -1;
+            st.lim[H] = (H == 0 || n < 8) && row < R ? G.L - T + (row - div_m(row, T_m) * T) : -1;
         }
 #pragma unroll
         for (int h = 0; h < NP; h++)
@@ -1381,7 +1383,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             const int phys_next = i + 1 < my ? tile_phys(G, G.c0 + ATP * (sl + AWAVES * (i + 1))) : 0;
             vm_wait<0>();    // this wave's half of tile i has landed
             __syncthreads(); // both halves of every slice's tile i are staged; every wave is done with tile i - 1
-            if (i + 1 < my) issue(SK, SV, G.c0, G.L, G.ws, G.g, G.ring0, i + 1, phys_next, par + i + 1);
+            if (i + 1 < my) issue(SK, SV, G.c0, G.L, G.ws, G.g, G.pbase, G.ring0, i + 1, phys_next, par + i + 1);
             if (i < my) {
                 const uint8_t * const sp = smem + stage(par + i) * SB;
                 RawTile<K2, V2> raw;
@@ -1397,7 +1399,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         // free: its tile my0 - 2 was read before that step's barrier)
         if (chain) {
             const ItemGeo N = item_geo(a, nxt);
-            if (N.ntiles > sl) issue(N.SK, N.SV, N.c0, N.L, N.ws, N.g, N.ring0, 0, tile_phys(N, N.c0 + ATP * sl), par + my0);
+            if (N.ntiles > sl) issue(N.SK, N.SV, N.c0, N.L, N.ws, N.g, N.pbase, N.ring0, 0, tile_phys(N, N.c0 + ATP * sl), par + my0);
         }
         asm volatile("" : "+v"(lane));
         n = lane & 15;

@@ -208,8 +208,9 @@ int mk_kv_ring_restore(void * h, int seq, int pos, const void * src, long long b
 /* Knobs: "max_blocks" caps the attention grid (0: one workgroup per work item); "occupancy" sets the decode
  * workgroups per CU for one-token calls on packed formats of at most 11 bits per K + V value: 0 (default) = three
  * when a launch has more work items than two per CU hold, else two; 2 or 3 = always that; "wide" (T >= 5): 1 = one
- * pass over K/V with 8-wave workgroups holding all 48 rows, 0 = two passes of 24 rows, 2 (default) = one pass when the
- * launch's K and V are q8, two passes for packed formats.  Results never depend on any of them. */
+ * pass over K/V with 8-wave workgroups holding all 48 rows, 0 = two passes of 24 rows (the second pass's tiles found in
+ * the same XCD's L2), 2 (default) = the faster of the two as measured, the two passes, on every format.  Results never
+ * depend on any of them. */
 int mk_kv_config(void * h, const char * key, long long value);
 
 /* Kernel timing with HIP events on the launch stream (the reference's MK_PROFILE per-phase means, engine.cu:382-506).

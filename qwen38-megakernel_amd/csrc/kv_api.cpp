@@ -597,7 +597,7 @@ static int attend_impl(void * h, int layer0, int n_layers, int n_seq, const int 
                 item += b.nl * NKV * b.sd[i].nseg;
             }
             b.n_base = item;
-            b.wide = a.R > 24 && (s.wide == 1 || (s.wide == 2 && kb == 8 && vb == 8));
+            b.wide = a.R > 24 && s.wide == 1; // (2, the default, runs the two batches: the faster form on every format measured)
             b.n_items = item * (b.wide ? 1 : (a.R + a.RP - 1) / a.RP);
             if (!prefetch) {
                 b.q = q + (size_t) l * n_seq * T * NH * qs;

@@ -10,13 +10,17 @@ namespace qkv {
 // work item x on workgroup x -- the same XCD (workgroups go round-robin over the XCDs by index) -- so its first tile
 // copies hit that L2 (or the last-level cache) instead of HBM.  No results: issued ahead of the attention, on another
 // stream beside independent work (the reference's pf_l2 in attn_proj, qwen38_mk.cu:2600-2621).
+// One workgroup per (sequence, layer, kv head, segment): the launch's n_base work items.  (An attention launch of
+// T = 5..8 in two 24-row batches has n_items = 2 n_base; batch b of item x is not item n_base + x, and an index past
+// n_base names a layer outside the launch.)  Item x's batches run on workgroups of x's XCD (kv_attn_decode.h), as x does
+// here.
 template <int KB, int VB>
 __global__ __launch_bounds__(256) void k_prefetch(AttnArgs a, int tiles) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const StoreLayout & S = a.S;
     const unsigned st_lds = (unsigned) __builtin_amdgcn_readfirstlane((unsigned) (size_t) (__attribute__((address_space(3))) uint8_t *) smem + wv * STAGE_BYTES);
-    for (int item = blockIdx.x; item < a.n_items; item += gridDim.x) {
+    for (int item = blockIdx.x; item < a.n_base; item += gridDim.x) {
         int si = 0;
         for (int i = 1; i < a.nseq; i++)
             if (item >= a.sd[i].item0) si = i;
@@ -736,7 +740,7 @@ static hipError_t prefetch_kb_vb(const AttnArgs & a, int tiles, hipStream_t st) 
         if (e != hipSuccess) return e;
         configured = true;
     }
-    hipLaunchKernelGGL((k_prefetch<KB, VB>), dim3(a.n_items), dim3(256), lds, st, a, tiles);
+    hipLaunchKernelGGL((k_prefetch<KB, VB>), dim3(a.n_base), dim3(256), lds, st, a, tiles);
     return hipGetLastError();
 }
 

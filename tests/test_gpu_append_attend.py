@@ -17,20 +17,22 @@ def step_inputs(rng, nseq, T, nl):
     return K, V
 
 
-@pytest.mark.parametrize("spec,win,lens,T,nl,f16,page", [
-    ("K*=5r,V*=6", 2048, [20000], 1, 1, True, 0),        # several tiles per wave, the new row in the last ring tile
-    ("K*=5r,V*=6", 2048, [40], 1, 2, False, 0),          # a short context: the new row in a wave's first tile
-    ("", 0, [1027], 8, 1, True, 0),                      # T = 8 (8-wave kernel), rows 1019..1026 straddle segment 1024
-    ("K*=5r,V*=6", 2048, [20000], 8, 1, True, 0),        # T = 8 on packed sides: two 24-row batches both store the rows
-    ("K0=4r,V0=7r,K1=8,V1=5", 640, [3190], 3, 2, False, 0),
-    ("K*=5r,V*=6", 1024, [2300, 700, 3100], 2, 1, True, 256),
+@pytest.mark.parametrize("spec,win,lens,T,nl,f16,page,wide", [
+    ("K*=5r,V*=6", 2048, [20000], 1, 1, True, 0, 2),     # several tiles per wave, the new row in the last ring tile
+    ("K*=5r,V*=6", 2048, [40], 1, 2, False, 0, 2),       # a short context: the new row in a wave's first tile
+    ("", 0, [1027], 8, 1, True, 0, 1),                   # T = 8 (8-wave kernel), rows 1019..1026 straddle segment 1024
+    ("", 0, [1027], 8, 1, True, 0, 2),                   # the same in the default form (two 24-row batches)
+    ("K*=5r,V*=6", 2048, [20000], 8, 1, True, 0, 2),     # T = 8 on packed sides: two 24-row batches both store the rows
+    ("K0=4r,V0=7r,K1=8,V1=5", 640, [3190], 3, 2, False, 0, 2),
+    ("K*=5r,V*=6", 1024, [2300, 700, 3100], 2, 1, True, 256, 2),
 ])
-def test_append_attend_equals_two_calls(qkv, torch_gpu, spec, win, lens, T, nl, f16, page):
+def test_append_attend_equals_two_calls(qkv, torch_gpu, spec, win, lens, T, nl, f16, page, wide):
     torch = torch_gpu
     rng = np.random.default_rng(70 + T + len(lens))
     nseq, ctx = len(lens), max(lens) + 64
     kw = dict(win=win, n_layers=nl, n_seq=nseq, ctx=ctx, page=page, n_pages=0)
     a, b = qkv.KVStore(spec, **kw), qkv.KVStore(spec, **kw)
+    b.config("wide", wide)
     if page:
         perm = rng.permutation(nseq * (-(-ctx // page)))
         npg = -(-ctx // page)

@@ -102,10 +102,12 @@ def test_wide_equals_batched(qkv, oracle, torch_gpu, spec, win, L, T):
     st.config("max_blocks", 0)
 
 
-@pytest.mark.parametrize("spec,win,L,T,tiles", [("K*=5r,V*=6", 2048, 20000, 1, 1), ("", 0, 9001, 8, 3), ("K*=4,V*=7r", 640, 5000, 2, 64)])
+@pytest.mark.parametrize("spec,win,L,T,tiles", [("K*=5r,V*=6", 2048, 20000, 1, 1), ("", 0, 9001, 8, 3), ("K*=4,V*=7r", 640, 5000, 2, 64),
+                                                ("K*=5r,V*=6", 2048, 20000, 8, 2)])
 def test_prefetch_changes_nothing(qkv, oracle, torch_gpu, spec, win, L, T, tiles):
     """mk_kv_prefetch (the attention's first tiles read into L2, on another stream) leaves every output bit as it was,
-    with window tiles, more tiles than a slice holds, and two layers; bad tile counts are refused."""
+    with window tiles, more tiles than a slice holds, two layers, and T = 8 as two 24-row batches (work items of the
+    attention launch that name the same segments); bad tile counts are refused."""
     torch = torch_gpu
     print(f"prefetch {spec} L={L} T={T} tiles={tiles}", flush=True)
     st, out, (K, V, Q) = check_case(qkv, oracle, torch, spec, win, L, T, nl=2, seed=31 + T, layers_checked=[])

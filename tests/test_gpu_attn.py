@@ -99,6 +99,8 @@ def test_wide_equals_batched(qkv, oracle, torch_gpu, spec, win, L, T):
     st.config("wide", 1)
     st.config("max_blocks", 37)
     assert np.array_equal(run_attend(torch, st, Q, [0], [L], T), out)
+    st.config("wide", 0)  # the row batches on a capped grid (workgroups walk the batch-paired work items)
+    assert np.array_equal(run_attend(torch, st, Q, [0], [L], T), out)
     st.config("max_blocks", 0)
 
 
@@ -187,6 +189,30 @@ def test_multi_sequence_paged(qkv, oracle, torch_gpu):
         flat = qkv.KVStore("K*=5r,V*=6", win=1024, n_layers=2, ctx=ctx)
         append_all(torch, flat, 0, K, V)
         assert np.array_equal(run_attend(torch, flat, Q[:, s:s + 1], [0], [L], 1)[:, 0], out[:, s]), s
+
+
+@pytest.mark.parametrize("T", [1, 8])
+def test_prefetch_multi_sequence_paged(qkv, oracle, torch_gpu, T):
+    """mk_kv_prefetch over several paged sequences (work items of three sequences, page-table lookups) changes no output
+    bit, at T = 1 and at T = 8 (row batches)."""
+    torch = torch_gpu
+    rng = np.random.default_rng(80 + T)
+    lens = [900, 2300, 3100]
+    ctx, page = 3328, 256
+    npg = ctx // page
+    st = qkv.KVStore("K*=5r,V*=6", win=1024, n_layers=2, n_seq=3, ctx=ctx, page=page, n_pages=3 * npg)
+    perm = rng.permutation(3 * npg)
+    for s, L in enumerate(lens):
+        st.set_pages(s, perm[s * npg:(s + 1) * npg])
+        K, V = synth_kv(rng, L, 2, outliers=True)
+        append_all(torch, st, s, K, V, chunks=[2048] * 2)
+    Q = rng.standard_normal((2, 3, T, NH, HD)).astype(np.float32)
+    out = run_attend(torch, st, Q, [0, 1, 2], lens, T)
+    assert np.isfinite(out).all()
+    side = torch.cuda.Stream()
+    st.prefetch(0, 2, [0, 1, 2], lens, T, 4, side.cuda_stream)
+    side.synchronize()
+    assert np.array_equal(run_attend(torch, st, Q, [0, 1, 2], lens, T), out)
 
 
 def test_verify_multi_sequence_paged(qkv, oracle, torch_gpu):

@@ -8,7 +8,7 @@ from kvcase import HD, NH, append_all, expected_attention, rel_err, synth_kv
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("spec,T", [("K*=5r,V*=6", 1), ("K*=5r,V*=5r", 3)])
+@pytest.mark.parametrize("spec,T", [("K*=5r,V*=6", 1), ("K*=5r,V*=5r", 3), ("K*=5r,V*=6", 8)])
 def test_gated_output_and_q32(qkv, oracle, torch_gpu, spec, T):
     torch = torch_gpu
     rng = np.random.default_rng(31)

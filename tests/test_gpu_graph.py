@@ -1,7 +1,8 @@
 """A decode step's one-layer mk_kv_attend calls captured as a HIP graph and replayed (how a serving loop issues them):
 every replay, with the program's own eager work and synchronizations between replays, gives the eager calls' output
 bit for bit -- the attention and combine launches record no memset nodes.  Preset F (packed K5r/V6 with the q8
-window) over several tiles per wave, T = 1 and T = 8 (the persistent verify kernel)."""
+window) over several tiles per wave, T = 1 and T = 8 in both verify forms (two 24-row batches, the default, and the
+persistent one-pass kernel)."""
 import numpy as np
 import pytest
 
@@ -10,12 +11,13 @@ from kvcase import HD, NH, append_all, synth_kv
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("T", [1, 8])
-def test_graph_replay_equals_eager(qkv, torch_gpu, T):
+@pytest.mark.parametrize("T,wide", [(1, 2), (8, 2), (8, 1)])
+def test_graph_replay_equals_eager(qkv, torch_gpu, T, wide):
     torch = torch_gpu
     rng = np.random.default_rng(90 + T)
     L, nl = 20000, 3
     st = qkv.KVStore("K*=5r,V*=6", win=2048, n_layers=nl, ctx=L)
+    st.config("wide", wide)
     K, V = synth_kv(rng, L, nl, outliers=True)
     append_all(torch, st, 0, K, V, chunks=[4096] * 8, f16=True)
     q = torch.from_numpy(rng.standard_normal((nl, 1, T, NH, HD)).astype(np.float32)).cuda()

@@ -54,7 +54,7 @@ def test_custom_rope_table(qkv, oracle, torch_gpu):
     st.close()
 
 
-@pytest.mark.parametrize("spec,T,n_seq", [("K*=5r,V*=6", 1, 1), ("K*=4,V*=5r", 3, 2)])
+@pytest.mark.parametrize("spec,T,n_seq", [("K*=5r,V*=6", 1, 1), ("K*=4,V*=5r", 3, 2), ("K*=5r,V*=6", 8, 2)])
 def test_attend_prep(qkv, oracle, torch_gpu, spec, T, n_seq):
     torch = torch_gpu
     rng = np.random.default_rng(23)

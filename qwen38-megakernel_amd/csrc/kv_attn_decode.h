@@ -251,8 +251,6 @@ __device__ __forceinline__ void vcodes_word(const VRaw<B> & v, int j, int w, uns
 #endif
 // NT = false: without the hint, for tiles that other work items read again (prefill row blocks of one key segment,
 // the row batches of one decode segment)
-// NT = false: without the hint, for tiles that other work items read again (prefill row blocks of one key segment,
-// the row batches of one decode segment)
 template <bool NT = true>
 __device__ __forceinline__ void dma16(const void * g, unsigned lds) {
     if constexpr (NT) asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" QKV_DMA_CPOL ::"s"(lds), "v"(g) : "memory");

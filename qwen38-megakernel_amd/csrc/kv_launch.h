@@ -49,8 +49,7 @@ struct AttnHead {
 static_assert(sizeof(AttnHead) == 208, "three 16-dword loads and one 4-dword load");
 
 struct AttnArgs {
-    AttnHead h;          // (k_attn's copy of the fields below, filled by fill_head)
-    // first: what a workgroup needs before its first tile copy, at fixed offsets (one round of scalar loads)
+    AttnHead h;          // the decode kernels' copy of fields below (fill_head); the others read the fields themselves
     SideLayout side0[2]; // K, V layouts of slot layer0 (S.side[layer0])
     StoreLayout S;
     int layer0;          // first slot of the launch

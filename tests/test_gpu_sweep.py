@@ -1,6 +1,7 @@
 """A seeded randomized sweep over the store and attention parameters: per case a random MK_KV spec (bits 4..8 per side,
 rotations), window, context length, T (capped to one 640-bucket as the reference's att_cap_T does), 1..3 sequences
-on a shared page pool with a shuffled page table, and the decode occupancy knob.  Every stored row is compared bit for bit and every attention
+on a shared page pool with a shuffled page table, the decode occupancy knob, a capped grid and an L2 prefetch of the
+call on a second stream.  Every stored row is compared bit for bit and every attention
 output within 2e-3 (max-abs relative) against the oracle.  QKV_SWEEP_CASES sets the number of cases (default 8);
 QKV_SWEEP_LONG_CASES the number of long-context cases (default 4)."""
 import os
@@ -37,11 +38,15 @@ def test_random_case(qkv, oracle, torch_gpu, case):
     T = min([qkv.cap_T(L - T, T) for L in lens] + [T])  # the T rows of every sequence stay inside one bucket
     T = max(T, 1)
     st = qkv.KVStore(spec, win=win, n_layers=1, n_seq=n_seq, ctx=ctx, page=page, n_pages=n_seq * npg)
-    occ = int(np.random.default_rng(5000 + case).choice([0, 3]))  # 3: small stages where the format allows
+    knobs = np.random.default_rng(5000 + case)
+    occ = int(knobs.choice([0, 3]))  # 3: small stages where the format allows
     st.config("occupancy", occ)
+    max_blocks = int(knobs.choice([0, 0, 1, 37, 255]))
+    st.config("max_blocks", max_blocks)
+    prefetch = bool(knobs.random() < 0.4)
     perm = rng.permutation(n_seq * npg)
     data = []
-    print(f"case {case}: spec={spec} win={win} lens={lens} T={T} occupancy={occ}", flush=True)
+    print(f"case {case}: spec={spec} win={win} lens={lens} T={T} occupancy={occ} max_blocks={max_blocks} prefetch={prefetch}", flush=True)
     for s, L in enumerate(lens):
         st.set_pages(s, perm[s * npg:(s + 1) * npg])
         K, V = synth_kv(rng, L, 1, outliers=bool(rng.random() < 0.5))
@@ -54,6 +59,10 @@ def test_random_case(qkv, oracle, torch_gpu, case):
     Q = rng.standard_normal((1, n_seq, T, NH, HD)).astype(np.float32)
     q = torch.from_numpy(Q).cuda()
     o = torch.full_like(q, float("nan"))
+    if prefetch:
+        side = torch.cuda.Stream()
+        st.prefetch(0, 1, list(range(n_seq)), lens, T, int(knobs.integers(1, 5)), side.cuda_stream)
+        side.synchronize()
     st.attend(0, 1, list(range(n_seq)), lens, T, q.data_ptr(), o.data_ptr())
     torch.cuda.synchronize()
     out = o.cpu().numpy()
@@ -69,7 +78,7 @@ def test_random_case(qkv, oracle, torch_gpu, case):
 @pytest.mark.parametrize("case", range(int(os.environ.get("QKV_SWEEP_LONG_CASES", "4"))))
 def test_random_long_case(qkv, oracle, torch_gpu, case):
     """The same sweep at long contexts (16,385 .. 70,000 positions: several tiles per wave, the window start inside a
-    segment), 1..2 paged sequences, and the verify form knob at T >= 5 (the forms give the same bits, so any may run)."""
+    segment), 1..2 paged sequences, and the verify form knob at T >= 5 (the forms give the same bits, so any may run), a capped grid and a prefetch of the call."""
     torch = torch_gpu
     rng = np.random.default_rng(7000 + case)
     spec = random_spec(rng)
@@ -87,9 +96,14 @@ def test_random_long_case(qkv, oracle, torch_gpu, case):
     wide = int(rng.choice([0, 1, 2]))
     st.config("occupancy", occ)
     st.config("wide", wide)
+    knobs = np.random.default_rng(9000 + case)
+    max_blocks = int(knobs.choice([0, 0, 7, 300]))
+    st.config("max_blocks", max_blocks)
+    prefetch = bool(knobs.random() < 0.5)
     perm = rng.permutation(n_seq * npg)
     data = []
-    print(f"long case {case}: spec={spec} win={win} lens={lens} T={T} occupancy={occ} wide={wide}", flush=True)
+    print(f"long case {case}: spec={spec} win={win} lens={lens} T={T} occupancy={occ} wide={wide} max_blocks={max_blocks} "
+          f"prefetch={prefetch}", flush=True)
     for s, L in enumerate(lens):
         st.set_pages(s, perm[s * npg:(s + 1) * npg])
         K, V = synth_kv(rng, L, 1, outliers=bool(rng.random() < 0.5))
@@ -104,6 +118,10 @@ def test_random_long_case(qkv, oracle, torch_gpu, case):
     Q = rng.standard_normal((1, n_seq, T, NH, HD)).astype(np.float32)
     q = torch.from_numpy(Q).cuda()
     o = torch.full_like(q, float("nan"))
+    if prefetch:
+        side = torch.cuda.Stream()
+        st.prefetch(0, 1, list(range(n_seq)), lens, T, int(knobs.integers(1, 9)), side.cuda_stream)
+        side.synchronize()
     st.attend(0, 1, list(range(n_seq)), lens, T, q.data_ptr(), o.data_ptr())
     torch.cuda.synchronize()
     out = o.cpu().numpy()

@@ -73,8 +73,9 @@ int mk_kv_attend(void * h, int layer0, int n_layers, int n_seq, const int * seqs
 
 /*
  * Prefetch for a later mk_kv_attend with the same (layer0, n_layers, seqs, lens, T): the first `tiles` (1..64) tiles
- * of every wave slice of every work item are read by a launch with the attention's grid and work-item order, so they
- * sit in the L2 of the XCD whose workgroup will stream them (and in the last-level cache).  Issue it on another
+ * of every wave slice of every segment are read by one workgroup per segment, placed on the XCD that the attention's
+ * workgroups for that segment (both row batches at T = 5..8) run on, so the tiles sit in that XCD's L2 (and in the
+ * last-level cache).  Issue it on another
  * stream beside independent work (the layer's projections) before the attention; it writes nothing.  Same checks as
  * mk_kv_attend.  Replaces the L2 prefetch of the first KV lines in attn_proj (pf_l2, qwen38_mk.cu:2600-2621).
  */

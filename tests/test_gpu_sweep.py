@@ -3,7 +3,8 @@ rotations), window, context length, T (capped to one 640-bucket as the reference
 on a shared page pool with a shuffled page table, the decode occupancy knob, a capped grid and an L2 prefetch of the
 call on a second stream.  Every stored row is compared bit for bit and every attention
 output within 2e-3 (max-abs relative) against the oracle.  QKV_SWEEP_CASES sets the number of cases (default 8);
-QKV_SWEEP_LONG_CASES the number of long-context cases (default 4)."""
+QKV_SWEEP_LONG_CASES the number of long-context cases (default 4), QKV_SWEEP_PREFILL_CASES the number of prefill cases
+(default 4)."""
 import os
 
 import numpy as np
@@ -132,3 +133,55 @@ def test_random_long_case(qkv, oracle, torch_gpu, case):
         ref = expected_attention(oracle, Q[0, s], K[:, 0], V[:, 0], T, kr, vr, kb, vb, ws, win > 0 and kb != 8, win > 0 and vb != 8)
         assert rel_err(out[0, s], ref) <= 2e-3, (case, spec, win, L, T)
     st.close()
+
+
+@pytest.mark.parametrize("case", range(int(os.environ.get("QKV_SWEEP_PREFILL_CASES", "4"))))
+def test_random_prefill_case(qkv, oracle, torch_gpu, case):
+    """Prefill under the same kind of draw: a random spec and window, 1 or 2 layers, a prompt of 1 .. 3,500 positions in
+    1 .. 4 random chunks, contiguous or on a permuted page pool.  The first and last 640-position pieces against the
+    oracle within 2e-3, the whole prompt in one chunk on a fresh store bitwise equal, the stored rows bit-exact."""
+    from test_gpu_prefill import pieces, run_prefill
+
+    torch = torch_gpu
+    rng = np.random.default_rng(11000 + case)
+    spec = random_spec(rng)
+    win = int(rng.choice([0, 256, 640, 2048]))
+    nl = int(rng.integers(1, 3))
+    P = int(rng.integers(1, 3501))
+    cuts = sorted(set(int(x) for x in rng.integers(1, P, size=int(rng.integers(0, 4))))) if P > 1 else []
+    chunks = [b - a for a, b in zip([0] + cuts, cuts + [P])]
+    paged = bool(rng.random() < 0.5)
+    print(f"prefill case {case}: spec={spec} win={win} nl={nl} P={P} chunks={chunks} paged={paged}", flush=True)
+    K, V = synth_kv(rng, P, nl, outliers=bool(rng.random() < 0.5))
+    Q = rng.standard_normal((nl, P, NH, HD)).astype(np.float32)
+    if paged:
+        page, ctx = 256, 3584
+        npg = ctx // page
+        st = qkv.KVStore(spec, win=win, n_layers=nl, n_seq=2, ctx=ctx, page=page, n_pages=2 * npg)
+        st.set_pages(1, rng.permutation(2 * npg)[:npg])
+        outs, p = [], 0
+        for c in chunks:
+            k = torch.from_numpy(np.ascontiguousarray(K[p:p + c])).cuda()
+            v = torch.from_numpy(np.ascontiguousarray(V[p:p + c])).cuda()
+            q = torch.from_numpy(np.ascontiguousarray(Q[:, p:p + c])).cuda()
+            o = torch.empty_like(q)
+            st.prefill(1, 0, nl, p, c, k.data_ptr(), v.data_ptr(), 0, q.data_ptr(), o.data_ptr())
+            torch.cuda.synchronize()
+            outs.append(o.cpu().numpy())
+            p += c
+        out = np.concatenate(outs, axis=1)
+        check_rows(oracle, st, K, V, seq=1, ring_from=max(0, P - qkv.ring_rows(win)) if win else 0)
+    else:
+        st, out = run_prefill(qkv, torch, spec, win, K, V, Q, chunks, P)
+        check_rows(oracle, st, K, V, ring_from=max(0, P - qkv.ring_rows(win)) if win else 0)
+    for l in range(nl):
+        kb, vb, kr, vr = st.kbits[l], st.vbits[l], st.krot[l], st.vrot[l]
+        for a, b in {pieces(P)[0], pieces(P)[-1]}:
+            ws = qkv.window_start(b, win)
+            ref = expected_attention(oracle, Q[l, a:b], K[:b, l], V[:b, l], b - a, kr, vr, kb, vb, ws, win > 0 and kb != 8,
+                                     win > 0 and vb != 8)
+            assert rel_err(out[l, a:b], ref) <= 2e-3, (case, spec, win, l, a, b)
+    st.close()
+    st2, out2 = run_prefill(qkv, torch, spec, win, K, V, Q, [P], P)
+    assert np.array_equal(out2, out), case
+    st2.close()

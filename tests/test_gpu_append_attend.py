@@ -23,6 +23,7 @@ def step_inputs(rng, nseq, T, nl):
     ("", 0, [1027], 8, 1, True, 0, 1),                   # T = 8 (8-wave kernel), rows 1019..1026 straddle segment 1024
     ("", 0, [1027], 8, 1, True, 0, 2),                   # the same in the default form (two 24-row batches)
     ("K*=5r,V*=6", 2048, [20000], 8, 1, True, 0, 2),     # T = 8 on packed sides: two 24-row batches both store the rows
+    ("K*=5r,V*=6", 2048, [20000], 8, 1, True, 0, 1),     # the same in one 8-wave pass
     ("K0=4r,V0=7r,K1=8,V1=5", 640, [3190], 3, 2, False, 0, 2),
     ("K*=5r,V*=6", 1024, [2300, 700, 3100], 2, 1, True, 256, 2),
 ])

@@ -289,3 +289,35 @@ def test_attend_rejects_unstored_and_evicted_rows(qkv, torch_gpu):
     append_all(torch, flat, 0, K, V)
     flat.attend(0, 1, [0], [1000], 1, q.data_ptr(), out.data_ptr())
     torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("T", [1, 8])
+def test_eight_sequences_per_call(qkv, oracle, torch_gpu, T):
+    """The most sequences one call takes (8) over a shared page pool, every sequence against the oracle; a ninth is
+    refused."""
+    torch = torch_gpu
+    rng = np.random.default_rng(60 + T)
+    lens = [int(x) for x in rng.integers(T + 40, 2400, 8)]
+    lens = [L - (L % 640) + 600 if qkv.cap_T(L - T, T) < T else L for L in lens]  # the T rows inside one bucket
+    ctx, page = 2560, 256
+    npg = ctx // page
+    st = qkv.KVStore("K*=5r,V*=6", win=512, n_layers=1, n_seq=9, ctx=ctx, page=page, n_pages=9 * npg)
+    perm = rng.permutation(9 * npg)
+    data = []
+    for s in range(9):
+        st.set_pages(s, perm[s * npg:(s + 1) * npg])
+    for s, L in enumerate(lens):
+        K, V = synth_kv(rng, L, 1, outliers=True)
+        append_all(torch, st, s, K, V)
+        data.append((K, V))
+    Q = rng.standard_normal((1, 8, T, NH, HD)).astype(np.float32)
+    out = run_attend(torch, st, Q, list(range(8)), lens, T)
+    for s, L in enumerate(lens):
+        K, V = data[s]
+        ref = expected_attention(oracle, Q[0, s], K[:, 0], V[:, 0], T, 1, 0, 5, 6, qkv.window_start(L, 512), True, True)
+        assert rel_err(out[0, s], ref) <= TOL, (s, L)
+    K, V = synth_kv(rng, 100, 1)
+    append_all(torch, st, 8, K, V)
+    q9 = torch.zeros((1, 9, 1, NH, HD), device="cuda")
+    with pytest.raises(qkv.KVError, match="sequences"):
+        st.attend(0, 1, list(range(9)), lens + [100], 1, q9.data_ptr(), q9.data_ptr())

@@ -321,3 +321,21 @@ def test_eight_sequences_per_call(qkv, oracle, torch_gpu, T):
     q9 = torch.zeros((1, 9, 1, NH, HD), device="cuda")
     with pytest.raises(qkv.KVError, match="sequences"):
         st.attend(0, 1, list(range(9)), lens + [100], 1, q9.data_ptr(), q9.data_ptr())
+
+
+def test_layer_window_of_a_17_slot_store(qkv, oracle, torch_gpu):
+    """A launch over slots 14..16 of a 17-slot store (the launch's first slot is not slot 0) equals the three one-slot
+    calls bitwise, and slot 16 matches the oracle."""
+    torch = torch_gpu
+    rng = np.random.default_rng(71)
+    L, nl = 3000, 17
+    st = qkv.KVStore("K*=5r,V*=6", win=1024, n_layers=nl, ctx=L)
+    K, V = synth_kv(rng, L, nl, outliers=True)
+    append_all(torch, st, 0, K, V)
+    Q = rng.standard_normal((3, 1, 1, NH, HD)).astype(np.float32)
+    out = run_attend(torch, st, Q, [0], [L], 1, layer0=14, nl=3)
+    for l in range(3):
+        one = run_attend(torch, st, Q[l:l + 1], [0], [L], 1, layer0=14 + l, nl=1)
+        assert np.array_equal(one[0], out[l]), l
+    ref = expected_attention(oracle, Q[2, 0], K[:, 16], V[:, 16], 1, 1, 0, 5, 6, qkv.window_start(L, 1024), True, True)
+    assert rel_err(out[2, 0], ref) <= TOL

@@ -264,6 +264,42 @@ __device__ __forceinline__ void dma16s(const void * base, unsigned voff, unsigne
         asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" QKV_DMA_CPOL ::"s"(lds), "v"(voff), "s"(base) : "memory");
     else asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds), "v"(voff), "s"(base) : "memory");
 }
+// N (1..4) consecutive 1 KiB pieces from one scalar base: M0 set once, the instruction offset (0, 1024, 2048, 3072)
+// added to both the global and the LDS address of each copy
+#define QKV_DMA_AT(O, C) "global_load_lds_dwordx4 %1, %2 offset:" #O C "\n\t"
+template <int N, bool NT = true>
+__device__ __forceinline__ void dma16s_run(const void * base, unsigned voff, unsigned lds) {
+    static_assert(N >= 1 && N <= 4, "one to four pieces");
+    if constexpr (NT) {
+        if constexpr (N == 1) asm volatile("s_mov_b32 m0, %0\n\t" QKV_DMA_AT(0, QKV_DMA_CPOL) ::"s"(lds), "v"(voff), "s"(base) : "memory");
+        if constexpr (N == 2)
+            asm volatile("s_mov_b32 m0, %0\n\t" QKV_DMA_AT(0, QKV_DMA_CPOL) QKV_DMA_AT(1024, QKV_DMA_CPOL) ::"s"(lds), "v"(voff), "s"(base) : "memory");
+        if constexpr (N == 3)
+            asm volatile("s_mov_b32 m0, %0\n\t" QKV_DMA_AT(0, QKV_DMA_CPOL) QKV_DMA_AT(1024, QKV_DMA_CPOL) QKV_DMA_AT(2048, QKV_DMA_CPOL)
+                         ::"s"(lds), "v"(voff), "s"(base) : "memory");
+        if constexpr (N == 4)
+            asm volatile("s_mov_b32 m0, %0\n\t" QKV_DMA_AT(0, QKV_DMA_CPOL) QKV_DMA_AT(1024, QKV_DMA_CPOL) QKV_DMA_AT(2048, QKV_DMA_CPOL)
+                             QKV_DMA_AT(3072, QKV_DMA_CPOL) ::"s"(lds), "v"(voff), "s"(base) : "memory");
+    } else {
+        if constexpr (N == 1) asm volatile("s_mov_b32 m0, %0\n\t" QKV_DMA_AT(0, "") ::"s"(lds), "v"(voff), "s"(base) : "memory");
+        if constexpr (N == 2) asm volatile("s_mov_b32 m0, %0\n\t" QKV_DMA_AT(0, "") QKV_DMA_AT(1024, "") ::"s"(lds), "v"(voff), "s"(base) : "memory");
+        if constexpr (N == 3)
+            asm volatile("s_mov_b32 m0, %0\n\t" QKV_DMA_AT(0, "") QKV_DMA_AT(1024, "") QKV_DMA_AT(2048, "") ::"s"(lds), "v"(voff), "s"(base) : "memory");
+        if constexpr (N == 4)
+            asm volatile("s_mov_b32 m0, %0\n\t" QKV_DMA_AT(0, "") QKV_DMA_AT(1024, "") QKV_DMA_AT(2048, "") QKV_DMA_AT(3072, "")
+                         ::"s"(lds), "v"(voff), "s"(base) : "memory");
+    }
+}
+// n pieces (compile time) from base into LDS at lds: runs of four
+template <int N, bool NT = true>
+__device__ __forceinline__ void dma16s_pieces(const uint8_t * base, unsigned voff, unsigned lds) {
+    if constexpr (N >= 4) {
+        dma16s_run<4, NT>(base, voff, lds);
+        if constexpr (N > 4) dma16s_pieces<N - 4, NT>(base + 4096, voff, lds + 4096);
+    } else if constexpr (N > 0) {
+        dma16s_run<N, NT>(base, voff, lds);
+    }
+}
 // a segment partial's four values, stored with the non-temporal hint: the combine reads them from beyond the L2 of the
 // XCD that wrote them (configs 3 fused, 4, 5: 1-2% shorter launches, the same bits)
 __device__ __forceinline__ void store_part(float * p, const float4 & y) {
@@ -342,12 +378,8 @@ __device__ __forceinline__ void issue_tile(const TileSrc & t, int nv, unsigned l
     constexpr bool DK = PART != 2, DV = PART != 1;
     if (nv == ATP) {
         const unsigned off = 16 * lane;
-        if constexpr (DK)
-#pragma unroll
-            for (int j = 0; j < KB; j++) dma16s<NT>(t.k + 1024 * j, off, lds + 1024 * j);
-        if constexpr (DV)
-#pragma unroll
-            for (int j = 0; j < VB; j++) dma16s<NT>(t.v + 1024 * j, off, lds + 1024 * (KB + j));
+        if constexpr (DK) dma16s_pieces<KB, NT>(t.k, off, lds);
+        if constexpr (DV) dma16s_pieces<VB, NT>(t.v, off, lds + 1024 * KB);
     } else {
         if constexpr (DK)
 #pragma unroll
@@ -381,8 +413,7 @@ __device__ __forceinline__ void issue_q8_part(const TileSrc & t, int nv, unsigne
     const uint8_t * const src = PART == 0 ? t.k : t.v;
     if (nv == ATP) {
         const unsigned off = 16 * lane;
-#pragma unroll
-        for (int j = 0; j < 8; j++) dma16s<NT>(src + 1024 * j, off, lds + 1024 * j);
+        dma16s_pieces<8, NT>(src, off, lds);
     } else {
 #pragma unroll
         for (int j = 0; j < 8; j++) {

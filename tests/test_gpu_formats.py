@@ -8,9 +8,10 @@ ring tiles in the segment holding the window start.  One store per format serves
 store's last T positions):
   T = 1 through the one-group kernel at two and at three workgroups per CU (the small-stage kernel where the format
         has one; the two must be equal bitwise);
-  T = 2 and 3 through the 16- and 24-row kernels;
-  T = 8 through the default verify form and through the other one (k_verify / two 24-row batches), bitwise equal,
-        and tokens 0 and 5 bitwise equal to one-token calls at their own lengths.
+  T = 2, 3 and 4 through the 16- and 24-row kernels;
+  T = 5 and 8 through the default verify form and through the other one (k_verify / two 24-row batches), bitwise
+        equal; at T = 8 tokens 0 and 5 bitwise equal to one-token calls at their own lengths.
+(T = 1, 2, 3, 4, 5, 8: the reference's own T set for this matrix.)
 One case at 200,031 positions (bucket 200,320, 13 tiles per wave) runs D at T = 1 and 8.  The prefill kernel of each
 format (k_prefill3, one instantiation per (K bits, V bits) pair as well) runs a 2,600-position prompt.
 """
@@ -90,7 +91,7 @@ def test_format_long_context(qkv, oracle, torch_gpu, name, spec, win):
     print(f"format {name} ({spec}, win {win}) L={L}", flush=True)
     rng, st, K, V = _store(qkv, torch, spec, win, L, 400 + len(name) * 7 + int(name.isdigit()) * 31 + win % 7)
     Kd, Vd = _operands(oracle, qkv, st, K, V, L, win)
-    for T in (1, 2, 3, 8):
+    for T in (1, 2, 3, 4, 5, 8):
         Q = rng.standard_normal((T, NH, HD)).astype(np.float32)
         out = _attend(torch, st, Q, L, T)
         e = rel_err(out, _expected(oracle, st, Q, Kd, Vd, T))
@@ -100,11 +101,12 @@ def test_format_long_context(qkv, oracle, torch_gpu, name, spec, win):
                 st.config("occupancy", occ)
                 assert np.array_equal(_attend(torch, st, Q, L, T), out), (name, "occupancy", occ)
             st.config("occupancy", 0)
-        if T == 8:
+        if T >= 5:
             for wide in (0, 1):
                 st.config("wide", wide)
                 assert np.array_equal(_attend(torch, st, Q, L, T), out), (name, "wide", wide)
             st.config("wide", 2)
+        if T == 8:
             # T-invariance (bench/dattn_bench.cu:1140-1160): token t equals a one-token call at its own length
             for t in (0, 5):
                 o1 = _attend(torch, st, Q[t:t + 1], L - T + t + 1, 1)

@@ -330,10 +330,11 @@ __device__ __forceinline__ void dequant_block(const uint8_t * row, uint16_t sc, 
     }
 }
 
-// fp16 tile layouts in LDS: K [32][SK_LD] (row = position), V transposed [256][SVT_LD] (row = dim) with the positions in
-// the order of the P V operands (position bits 2 and 3 swapped)
+// fp16 tile layout in LDS: K and V as [32][SK_LD] (row = position; the consumers read V transposed, read_tr16)
 constexpr int SK_LD = HD + 8;
-constexpr int SVT_LD = ATP + 8;
+// V rows 560 bytes apart: the 4 rows that one 16-lane group of a transposed read addresses (32 bytes each) start 32
+// bytes apart in the banks instead of overlapping (528 bytes: 3.6% slower; 576: 4% slower; 592: the same as 560)
+constexpr int SV_LD = HD + 24;
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 // Prefill attention on 32x32x16 MFMAs: workgroup = (128 query rows, kv head, key segment), row block fastest so the
@@ -343,9 +344,36 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 // buffer.  One barrier per tile hands a buffer over; on each SIMD a producer's VALU work overlaps a consumer's MFMAs.
 constexpr int PQ_REGION = 5120;                           // per producer and stage: K rows 2 KB, V rows 2 KB, scales 1 KB
 constexpr int PQ_STAGES = 2 * 4 * PQ_REGION;              // two stages of the 4 producers
-constexpr int PQ_BUF = (ATP * SK_LD + HD * SVT_LD + 64) * 2; // one fp16 tile: K [32][SK_LD], V^T [256][SVT_LD] + skew
-// V^T row r starts at r SVT_LD + 8 (r / 32): the 8 rows a producer wave writes at once (32 apart) fall in different banks
+constexpr int PQ_BUF = ATP * (SK_LD + SV_LD) * 2;        // one fp16 tile: K [32][SK_LD], V [32][SV_LD]
 constexpr int PQ_LDS = PQ_STAGES + 2 * PQ_BUF;
+
+typedef __fp16 f16v4 __attribute__((__vector_size__(4 * sizeof(__fp16))));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+// ds_read_b64_tr_b16 at LDS byte address off: in each group of 16 lanes, lane i receives element i % 4 of the 8-byte
+// pieces addressed by lanes i / 4 + 4 j, j = 0..3 (as element j)
+__device__ __forceinline__ half4 read_tr16(unsigned off) {
+    return __builtin_bit_cast(half4, __builtin_amdgcn_ds_read_tr16_b64_v4f16((__attribute__((address_space(3))) f16v4 *) (size_t) off));
+}
+
+// Instruction order for an unrolled chain of N LDS fragment reads each feeding one MFMA: the first D reads, then one
+// MFMA and the next read in turn, then the last D MFMAs (scheduling groups; no effect on the arithmetic).  Left to
+// itself the scheduler reads each fragment just before its MFMA into the same registers, so every MFMA of the chain
+// waits a whole LDS round trip.
+// K: 3 fragments ahead; V: 2 MFMAs ahead (4 transposed reads).  Measured: K 2 ahead 1.3% slower, V 3 or 4 ahead
+// 1.1% and 0.3% slower.
+constexpr int PF_K = 3, PF_V = 2;
+template <int D, int N, int RPM = 1>
+__device__ __forceinline__ void pipeline_reads() {
+    if constexpr (D > 0) {
+        __builtin_amdgcn_sched_group_barrier(0x100, D * RPM, 0); // DS reads
+#pragma unroll
+        for (int i = 0; i < N - D; i++) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0); // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x100, RPM, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, D, 0);
+    }
+}
 static_assert(PQ_LDS >= PF2_ROWS * SK_LD * 2, "query staging inside the tile buffers");
 
 // the 8 positions of quarter pw of tile i: one producer wave's copies (5 instructions, always) into its region
@@ -370,7 +398,7 @@ __device__ __forceinline__ void pq_issue(const TileSrc & t, int nq, unsigned lds
 
 // one producer lane: position lane % 8 of its quarter, scale block lane / 8, K and V into the fp16 buffer
 template <int KB, int VB>
-__device__ __forceinline__ void pq_dequant(const uint8_t * reg, int pw, int lane, _Float16 * sK, _Float16 * sVt) {
+__device__ __forceinline__ void pq_dequant(const uint8_t * reg, int pw, int lane, _Float16 * sK, _Float16 * sV) {
     const int pl = lane & 7, b = lane >> 3, p = 8 * pw + pl;
     const uint16_t * ksc = reinterpret_cast<const uint16_t *>(reg + 4096);
     half2v o[16];
@@ -379,13 +407,9 @@ __device__ __forceinline__ void pq_dequant(const uint8_t * reg, int pw, int lane
 #pragma unroll
     for (int k = 0; k < 4; k++) kd[k] = make_uint4(as_u(o[4 * k]), as_u(o[4 * k + 1]), as_u(o[4 * k + 2]), as_u(o[4 * k + 3]));
     dequant_block<VB>(reg + 2048 + pl * 32 * VB, ksc[64 + pl * 8 + b], b, o);
-    const int x = (p & ~12) | ((p >> 1) & 4) | ((p << 1) & 8);
-    _Float16 * vd = sVt + (32 * b) * SVT_LD + 8 * b + x;
+    uint4 * vd = reinterpret_cast<uint4 *>(sV + p * SV_LD + 32 * b);
 #pragma unroll
-    for (int k = 0; k < 16; k++) {
-        vd[(2 * k) * SVT_LD] = o[k][0];
-        vd[(2 * k + 1) * SVT_LD] = o[k][1];
-    }
+    for (int k = 0; k < 4; k++) vd[k] = make_uint4(as_u(o[4 * k]), as_u(o[4 * k + 1]), as_u(o[4 * k + 2]), as_u(o[4 * k + 3]));
 }
 
 template <int KB, int VB>
@@ -425,9 +449,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     auto dequant = [&](int i) {
         const uint8_t * reg = smem + ((i & 1) * 4 + pw) * PQ_REGION;
         _Float16 * sK = buf0 + (i & 1) * (PQ_BUF / 2);
-        _Float16 * sVt = sK + ATP * SK_LD;
-        if (is_ring(i)) pq_dequant<8, 8>(reg, pw, lane, sK, sVt);
-        else pq_dequant<KB, VB>(reg, pw, lane, sK, sVt);
+        _Float16 * sV = sK + ATP * SK_LD;
+        if (is_ring(i)) pq_dequant<8, 8>(reg, pw, lane, sK, sV);
+        else pq_dequant<KB, VB>(reg, pw, lane, sK, sV);
     };
     // ---- query rows: all 8 waves stage 16 rows each (prep, FWHT for rotated K, * 1/16, fp16), consumers take fragments;
     // loaded 8 rows at a time (independent loads, one wait)
@@ -461,6 +485,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     __syncthreads();
     // Both roles pass the same barriers: two after the staging, then one per tile.
     if (producer) {
+        // the producers set the pace (their dequantization and fp16 tile writes take longer per tile than a consumer's
+        // MFMAs and softmax): on a SIMD shared with a consumer, the arbiter's preference for the older wave (the
+        // consumer) would otherwise give the consumer's issue slots first
+        __builtin_amdgcn_s_setprio(1);
         __syncthreads(); // the consumers hold their query fragments: the staging area is free
         issue(0);
         if (ntiles > 1) issue(1);
@@ -499,7 +527,13 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     constexpr float RESCALE_LOG2 = 8.f;
     for (int i = 0; i < ntiles; i++) {
         const _Float16 * const sK = buf0 + (i & 1) * (PQ_BUF / 2);
-        const _Float16 * const sVt = sK + ATP * SK_LD;
+        const _Float16 * const sV = sK + ATP * SK_LD;
+        // V operand of O^T += V^T P^T (lane l: dim 32 db + l % 32, the 8 positions of P's k order for half hf) by two
+        // transposed reads of 4 positions: lane a = q + 4 j of each 16-lane group g addresses position 16 s2 + 4 hf + j
+        // (+ 8 for the second read), dims 32 db + 16 (g & 1) + 4 q .. + 3, and lane i of the group receives dim
+        // 32 db + 16 (g & 1) + i of the 4 positions
+        const unsigned v_lane = (unsigned) (size_t) (const __attribute__((address_space(3))) _Float16 *) sV +
+                                2 * ((4 * hf + ((lane >> 2) & 3)) * SV_LD + 16 * ((lane >> 4) & 1) + 4 * (lane & 3));
         const int p0 = c0 + ATP * i;
         f32x16 sacc;
 #pragma unroll
@@ -509,13 +543,24 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             const half8 ak = *reinterpret_cast<const half8 *>(sK + c * SK_LD + 16 * ks + 8 * hf);
             sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(ak, qf[ks], sacc, 0, 0, 0);
         }
-        const bool full = p0 + ATP - 1 <= lim_min;
+        // the K fragments are read PF_K ahead of their MFMAs: each read's LDS latency then hides behind the MFMAs
+        // already issued instead of standing between two MFMAs of the chain
+        pipeline_reads<PF_K, 16>();
+        // fully visible tiles (wave-uniform) skip the causal mask
         float mx = -INFINITY;
+        if (p0 + ATP - 1 <= lim_min) {
 #pragma unroll
-        for (int e = 0; e < 16; e++) {
-            const int pos = p0 + 8 * (e >> 2) + 4 * hf + (e & 3);
-            sacc[e] = full || pos <= lim ? sacc[e] * LOG2E : -INFINITY;
-            mx = fmaxf(mx, sacc[e]);
+            for (int e = 0; e < 16; e++) {
+                sacc[e] = sacc[e] * LOG2E;
+                mx = fmaxf(mx, sacc[e]);
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 16; e++) {
+                const int pos = p0 + 8 * (e >> 2) + 4 * hf + (e & 3);
+                sacc[e] = pos <= lim ? sacc[e] * LOG2E : -INFINITY;
+                mx = fmaxf(mx, sacc[e]);
+            }
         }
         mx = fmaxf(mx, shfl_xor(mx, 32));
         const float mnew = mx > m + RESCALE_LOG2 ? mx : m;
@@ -548,9 +593,11 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         for (int db = 0; db < 8; db++)
 #pragma unroll
             for (int s2 = 0; s2 < 2; s2++) {
-                const half8 av = *reinterpret_cast<const half8 *>(sVt + (32 * db + c) * SVT_LD + 8 * db + 16 * s2 + 8 * hf);
+                const unsigned vo = v_lane + 2 * ((16 * s2) * SV_LD + 32 * db);
+                const half8 av = __builtin_shufflevector(read_tr16(vo), read_tr16(vo + 2 * 8 * SV_LD), 0, 1, 2, 3, 4, 5, 6, 7);
                 O[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, pb[s2], O[db], 0, 0, 0);
             }
+        pipeline_reads<PF_V, 16, 2>(); // (the score registers are free here: the V fragments have room to run further ahead)
         __syncthreads(); // buffer i % 2 free for the producers
     }
     if (row < a.R) {

@@ -623,19 +623,34 @@ __global__ __launch_bounds__(256) void k_prefill_combine(PrefillArgs a) {
     const int nk = pos / a.seg + 1;
     float M = -INFINITY, den = 0.f;
     float4 num = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int k = 0; k < nk; k++) {
-        const size_t u = (size_t) (g * a.nseg + k) * a.R + r;
-        const float2 ml = a.ml[u];
-        const float4 o = *reinterpret_cast<const float4 *>(a.part + u * HD + 4 * lane);
-        const float Mn = fmaxf(M, ml.x);
-        const float e0 = M == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(M - Mn);
-        const float e1 = ml.x == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ml.x - Mn);
-        num.x = __builtin_fmaf(num.x, e0, e1 * o.x);
-        num.y = __builtin_fmaf(num.y, e0, e1 * o.y);
-        num.z = __builtin_fmaf(num.z, e0, e1 * o.z);
-        num.w = __builtin_fmaf(num.w, e0, e1 * o.w);
-        den = __builtin_fmaf(den, e0, e1 * ml.y);
-        M = Mn;
+    // up to 8 segments' partials loaded in one round, then folded in order (the fold is the same sequence of operations
+    // as one segment at a time)
+    constexpr int RND = 8;
+    for (int k0 = 0; k0 < nk; k0 += RND) {
+        float2 mls[RND];
+        float4 os[RND];
+#pragma unroll
+        for (int j = 0; j < RND; j++)
+            if (k0 + j < nk) {
+                const size_t u = (size_t) (g * a.nseg + k0 + j) * a.R + r;
+                mls[j] = a.ml[u];
+                os[j] = *reinterpret_cast<const float4 *>(a.part + u * HD + 4 * lane);
+            }
+#pragma unroll
+        for (int j = 0; j < RND; j++)
+            if (k0 + j < nk) {
+                const float2 ml = mls[j];
+                const float4 o = os[j];
+                const float Mn = fmaxf(M, ml.x);
+                const float e0 = M == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(M - Mn);
+                const float e1 = ml.x == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ml.x - Mn);
+                num.x = __builtin_fmaf(num.x, e0, e1 * o.x);
+                num.y = __builtin_fmaf(num.y, e0, e1 * o.y);
+                num.z = __builtin_fmaf(num.z, e0, e1 * o.z);
+                num.w = __builtin_fmaf(num.w, e0, e1 * o.w);
+                den = __builtin_fmaf(den, e0, e1 * ml.y);
+                M = Mn;
+            }
     }
     float v[4] = {num.x / den, num.y / den, num.z / den, num.w / den};
     const int h = GQA * g + hh;

@@ -144,12 +144,15 @@ struct PrefillArgs {
     float * part;      // [NKV][nseg][R][HD] per-segment partial outputs (unnormalised)
     float2 * ml;       // [NKV][nseg][R] (max in log2 units, sum)
 };
-// key positions per prefill segment: 2,048 ceil(Lb / 32,768) with Lb = L rounded up to its 640-bucket, so at most 16
-// segments per row (the partials stay small at long contexts) and the same segments for every row of a bucket (every
-// row's result is a function of its position)
+// key positions per prefill segment: 128 ceil(Lb / 256) with Lb = L rounded up to its 640-bucket: two segments per row
+// at most, the same segments for every row of a bucket (every row's result is a function of its position).  A full
+// 640-position piece then runs 30 row blocks x 4 kv heads x 2 segments = 240 workgroups, one round on 256 CUs at one
+// workgroup per CU; more segments repeat each workgroup's query staging and partial stores (about 4 segments: 9% slower
+// on a 16,384-position prompt, about 8: 23%; odd counts leave a partial round: about 3 segments 21% slower; one
+// segment uses half the CUs: 39% slower)
 inline int pf_seg(int L) {
     const int lb = (L + ATT_BUCKET - 1) / ATT_BUCKET * ATT_BUCKET;
-    return 2048 * ((lb + 32767) / 32768);
+    return 128 * ((lb + 255) / 256);
 }
 constexpr int PF2_ROWS = 128; // query rows per prefill workgroup (32 per wave)
 

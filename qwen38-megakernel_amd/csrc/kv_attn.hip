@@ -431,18 +431,32 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const int ntiles = (c1 - c0 + ATP - 1) / ATP;
     const unsigned lds0 = (unsigned) (size_t) (__attribute__((address_space(3))) uint8_t *) smem;
     _Float16 * const buf0 = reinterpret_cast<_Float16 *>(smem + PQ_STAGES);
-    const SideLayout & SK = S.side[a.layer][0];
-    const SideLayout & SV = S.side[a.layer][1];
+    // by value: held in registers, not re-read from the kernel arguments for every tile
+    const SideLayout SK = S.side[a.layer][0];
+    const SideLayout SV = S.side[a.layer][1];
     const size_t ring0 = (size_t) (a.seq * NKV + g) * S.kvrc;
     const int L = a.L, ws = a.ws;
     auto is_ring = [&](int i) { return S.kvrc > 0 && c0 + ATP * i >= ws; };
+    // the producer's tiles are issued in order 0, 1, 2, ..: the page and offset of the next one are tracked (a tile
+    // never straddles a page: pages hold a multiple of 32 positions), and a page's physical index is looked up when the
+    // previous tile ends the previous page, one tile before its copies are issued
+    const int * const pt = S.ptab + (size_t) a.seq * S.pt_stride;
+    int nx_lp = c0 / S.page, nx_off = c0 - nx_lp * S.page;
+    int nx_phys = ((const_int_p) pt)[nx_lp];
     // producer: the copies of quarter pw of tile i into stage i % 2
     auto issue = [&](int i) {
         const int p0t = c0 + ATP * i, nv = min(ATP, L - p0t);
         const int q0 = min(8 * pw, nv - 1), nq = min(8, nv - q0), p0 = p0t + q0;
         const unsigned lds = (unsigned) __builtin_amdgcn_readfirstlane(lds0 + ((i & 1) * 4 + pw) * PQ_REGION);
         const bool ring = is_ring(i);
-        const TileSrc t = tile_src<KB, VB>(S, SK, SV, g, p0, page_of(S, a.seq, p0), ring0, ring);
+        const size_t mr = (size_t) (g * S.n_pages + nx_phys) * S.page + nx_off + q0;
+        nx_off += ATP;
+        if (nx_off == S.page) {
+            nx_off = 0;
+            nx_lp++;
+            if (i + 1 < ntiles) nx_phys = ((const_int_p) pt)[nx_lp];
+        }
+        const TileSrc t = tile_src_row<KB, VB>(S.kvrc, SK, SV, !ring || !SK.ring || !SV.ring ? mr : 0, p0, ring0, ring);
         if (ring) pq_issue<8, 8>(t, nq, lds, lane);
         else pq_issue<KB, VB>(t, nq, lds, lane);
     };

@@ -60,8 +60,8 @@ def test_prefill_parity_and_chunking(qkv, oracle, torch_gpu, spec, win):
 
 
 def test_prefill_two_segments_then_decode(qkv, oracle, torch_gpu):
-    """A 9,000-position context over five 2,048-position key segments (the combine folds up to five), then a decode step
-    on the same store."""
+    """A 9,000-position context (the last pieces over two key segments of 4,864 positions, the combine folding both),
+    then a decode step on the same store."""
     torch = torch_gpu
     rng = np.random.default_rng(42)
     P, nl, win, spec = 9000, 1, 2048, "K*=5r,V*=6"
@@ -148,16 +148,19 @@ def test_prefill_errors(qkv, torch_gpu):
     st.close()
 
 
-def test_prefill_paged_equals_contiguous(qkv, torch_gpu):
-    """Prefill on a shared page pool with a permuted page table gives the contiguous store's outputs bit for bit."""
+@pytest.mark.parametrize("page", [256, 32, 96])
+def test_prefill_paged_equals_contiguous(qkv, torch_gpu, page):
+    """Prefill on a shared page pool with a permuted page table gives the contiguous store's outputs bit for bit.  The
+    kernel's copy side follows its tiles from page to page: 32-position pages change page at every tile, and 96-position
+    pages put the second key segment's start (position 1,024 of the last pieces) inside a page."""
     torch = torch_gpu
     rng = np.random.default_rng(44)
-    P, nl, win, spec, page = 1500, 1, 512, "K*=5r,V*=6", 256
+    P, nl, win, spec = 1500, 1, 512, "K*=5r,V*=6"
     K, V = synth_kv(rng, P, nl, outliers=True)
     Q = rng.standard_normal((nl, P, NH, HD)).astype(np.float32)
     st, ref = run_prefill(qkv, torch, spec, win, K, V, Q, [900, 600], 2048)
     st.close()
-    npg = 2048 // page
+    npg = -(-2048 // page)
     paged = qkv.KVStore(spec, win=win, n_layers=nl, n_seq=2, ctx=2048, page=page, n_pages=2 * npg)
     perm = np.random.default_rng(7).permutation(2 * npg)
     paged.set_pages(1, perm[:npg])
